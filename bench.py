@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""Decode-token-path benchmark on one MI355X.
+
+Default workload (the headline metric): top-p sampling of B=1024 rows over a
+V=65536 bf16 vocabulary (Zipf-like logits, T=0.6, p=0.95, top-k off).  A "step"
+is one lsg_sample launch over one batch.  Inputs are resident in HBM before the
+timed region; the timed region replays a HIP graph of K launches that rotate
+over NBUF distinct logits buffers (> 512 MB in total, so the 256 MB Infinity
+Cache cannot serve them), bracketed by torch.cuda.synchronize() and timed with
+HIP events on the launch stream.
+
+Prints one JSON line (metric / value / roofline / cpu_baseline ...).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                  [--no-cpu-baseline]
+Workloads: sample_huginn (default), sample_ouro, gate_cdb, cdb_mixed_depth.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "sampled rows/sec and achieved HBM GB/s (% of peak) at batch 1024, vocab 65536"
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="sample_huginn",
+                    choices=["sample_huginn", "sample_ouro", "gate_cdb", "cdb_mixed_depth"])
+    ap.add_argument("--nbuf", type=int, default=0, help="logits buffers rotated (0: auto, > 512 MB)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU baseline sample (0: auto)")
+    return ap.parse_args()
+
+
+def _traffic_from_profiles(workload: str):
+    """HBM bytes per launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), if a summary has been recorded."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def _time_graph(torch, launch, nlaunch: int, warmup: int):
+    """Warm up eagerly, capture nlaunch launches in one graph, time one replay."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for i in range(nlaunch):
+            launch(i)
+    torch.cuda.synchronize()
+    graph.replay()  # untimed replay: graph upload
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3  # seconds
+
+
+def _cpu_baseline_sampling(wl, rows: int):
+    import numpy as np
+
+    import oracle
+
+    x = wl["logits"][:rows].cpu()
+    arr = x.numpy() if x.dtype.itemsize == 4 else oracle.bf16_bits(x)
+    code = oracle.F32 if x.dtype.itemsize == 4 else oracle.BF16
+    sel = lambda t: None if t is None else t[:rows].cpu().numpy()
+    threads = 1
+    t0 = time.perf_counter()
+    oracle.sample(arr, sel(wl["temperatures"]), sel(wl.get("top_k")), sel(wl["top_p"]), sel(wl["uniforms"]),
+                  dtype=code, nthreads=threads)
+    dt = time.perf_counter() - t0
+    del np
+    return rows / dt, threads
+
+
+def main():
+    a = _parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {a.gpus}); the sampler shards rows across GPUs "
+              "with no exchange, so run one process per GPU.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.package()
+    wlmod = pkg.workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    K, W = a.steps, a.warmup
+
+    if a.workload in ("sample_huginn", "sample_ouro", "cdb_mixed_depth"):
+        if a.workload == "sample_huginn":
+            make = lambda seed: wlmod.sample_huginn(dev, seed=seed)
+            desc = "sample_huginn: B=1024 V=65536 bf16 Zipf-like logits, T=0.6 top_p=0.95 top_k off"
+        elif a.workload == "sample_ouro":
+            make = lambda seed: wlmod.sample_ouro(dev, seed=seed)
+            desc = "sample_ouro: B=256 V=49152 bf16 logits=hW^T, mixed T/top_k/top_p"
+        else:
+            make = lambda seed: wlmod.cdb_mixed_depth(dev, seed=seed)
+            desc = "cdb_mixed_depth sampling: B=2048 V=65536 fp32 Student-t, mixed greedy/top_k/top_p"
+        wl = make(3 if a.workload == "sample_huginn" else 1)
+        x0 = wl["logits"]
+        B, V = x0.shape
+        buf_bytes = x0.numel() * x0.element_size()
+        nbuf = a.nbuf or max(3, -(-(600 << 20) // buf_bytes))
+        bufs = [x0] + [make(100 + i)["logits"] for i in range(nbuf - 1)]
+        T, Kt, P, U = wl["temperatures"], wl.get("top_k"), wl["top_p"], wl["uniforms"]
+        outs = [torch.empty(B, dtype=torch.int32, device=dev) for _ in range(nbuf)]
+
+        def launch(i):
+            pkg.sample_rows(bufs[i % nbuf], T, Kt, P, U, out=outs[i % nbuf])
+
+        secs = _time_graph(torch, launch, K, W)
+        n_params = 2 + (Kt is not None)  # temperature, top_p (+ top_k) per row
+        alg = wlmod.algorithmic_bytes_sampling(B, V, x0.element_size(), n_params)
+        rows_per_s = B * K / secs
+        per_launch = secs / K
+        cpu = None
+        if not a.no_cpu_baseline:
+            rows = a.cpu_rows or min(B, 256)
+            v, cores = _cpu_baseline_sampling(wl, rows)
+            cpu = {"value": v, "unit": "rows/s", "cores": cores, "kind": "port",
+                   "sample": f"first {rows} rows of the same {B}x{V} workload, float64 C oracle, 1 thread"}
+        result = {
+            "metric": METRIC,
+            "value": rows_per_s,
+            "unit": "rows/s",
+            "n_gpus": 1,
+            "steps": K,
+            "warmup": W,
+            "ms_per_step": per_launch * 1e3,
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "f32",
+            "data": "synthetic",
+            "config": {"workload": desc, "batch": B, "vocab": V, "logits_dtype": str(x0.dtype).split(".")[-1],
+                       "rotated_buffers": nbuf, "rotated_bytes": nbuf * buf_bytes},
+            "roofline": {
+                "bound": "hbm",
+                "achieved": alg / per_launch / 1e9,
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": alg / per_launch / 1e9 / HBM_PEAK_GBS,
+                "traffic": _traffic_from_profiles(a.workload),
+            },
+            "cpu_baseline": cpu,
+        }
+    else:  # gate_cdb: the 4-step exit gate with compaction (latency-bound)
+        wl = wlmod.gate_cdb(dev)
+        gate = pkg.OuroExitGate(wl["weight"], wl["bias"], exit_threshold=wl["tau"], loop_steps=4)
+        B, H = wl["hidden"][0].shape
+        nset = 64  # 64 x 4 steps x 2 MiB hidden states rotate through > 512 MB
+        hs = [torch.randn(B, H, device=dev).to(torch.bfloat16) for _ in range(nset)]
+        F = torch.zeros(B, device=dev)
+
+        def launch(i):
+            gate.exit_signal_compact(hs[i % nset], F, i % 4)
+
+        secs = _time_graph(torch, launch, K, W)
+        per = secs / K
+        alg = wlmod.algorithmic_bytes_gate(B, H)
+        result = {
+            "metric": "exit-gate steps/sec (B=512, H=2048 bf16, with compaction)",
+            "value": K / secs, "unit": "steps/s", "n_gpus": 1, "steps": K, "warmup": W,
+            "ms_per_step": per * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "gate_cdb: B=512 H=2048 bf16, tau=0.2, 4 loop steps", "batch": B, "hidden": H},
+            "roofline": {"bound": "hbm", "achieved": alg / per / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": alg / per / 1e9 / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(a.workload)},
+            "cpu_baseline": None,
+        }
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,56 @@
+"""The fused CDB decode step (gate -> device compaction -> sampling of the
+exited rows) against the oracle composed the same way."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _arr(orc, t):
+    t = t.detach().cpu().contiguous()
+    return t.numpy() if t.dtype == torch.float32 else orc.bf16_bits(t)
+
+
+def test_mixed_depth_decode_step(lsg, orc, dev):
+    """B=2048 rows at depths 1-4, fp32 logits V=65536, gate tau=0.2; exited rows
+    sample with mixed greedy/top-k/top-p parameters."""
+    wl = lsg.workloads.cdb_mixed_depth(dev)
+    gate = lsg.OuroExitGate(wl["weight"], wl["bias"], exit_threshold=wl["tau"], loop_steps=4)
+    args = lsg.BatchSamplingArgs(wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+    res = lsg.cdb_decode_step(gate, wl["hidden"], wl["F_prev"], wl["loop_step"], wl["logits"], args)
+    torch.cuda.synchronize()
+    B = wl["logits"].shape[0]
+    ref = orc.exit_gate(_arr(orc, wl["hidden"]), _arr(orc, wl["weight"]), _arr(orc, wl["bias"]),
+                        wl["F_prev"].cpu().numpy(), wl["loop_step"].cpu().numpy(), wl["tau"], dtype=orc.BF16)
+    mask = res.signal.cpu().numpy()
+    clean = (ref["amb"] & 1) == 0
+    assert np.array_equal(mask[clean].astype(np.uint8), ref["mask"][clean])
+    n = int(res.n_exit.item())
+    exit_idx = res.exit_idx[:n].cpu().numpy()
+    assert np.array_equal(exit_idx, np.nonzero(mask)[0])
+    assert n > 0
+    rows = exit_idx
+    x = wl["logits"][torch.from_numpy(rows).to(dev).long()].cpu().numpy()
+    sel = lambda t: t.cpu().numpy()[rows]
+    want, amb = orc.sample(x, sel(wl["temperatures"]), sel(wl["top_k"]), sel(wl["top_p"]),
+                           sel(wl["uniforms"]))
+    got = res.token_ids[:n].cpu().numpy()
+    bad = (got != want) & (amb == 0)
+    assert not bad.any(), np.nonzero(bad)
+
+
+def test_gate_then_greedy(lsg, dev):
+    """The CDB gate workload: exited rows greedy-sampled from bf16 logits."""
+    wl = lsg.workloads.gate_cdb(dev)
+    gate = lsg.OuroExitGate(wl["weight"], wl["bias"], exit_threshold=wl["tau"], loop_steps=4)
+    F = None
+    for step, h in enumerate(wl["hidden"]):
+        res = lsg.cdb_decode_step(gate, h, F, step, wl["logits"], lsg.BatchSamplingArgs(None))
+        n = int(res.n_exit.item())
+        rows = res.exit_idx[:n].long()
+        want = torch.argmax(wl["logits"][rows], dim=-1).to(torch.int32)
+        assert torch.equal(res.token_ids[:n], want)
+        F = res.state

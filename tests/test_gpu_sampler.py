@@ -1,0 +1,268 @@
+"""Parity of the HIP sampler (lsg_sample) with the CPU oracle and torch.argmax.
+
+Bar: greedy ids bit-exact; sampled ids equal except on rows the oracle flags as
+ambiguous (CDF within 1e-6 of the uniform, or top-p mass within 1e-6 of p).
+"""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _host(orc, logits):
+    x = logits.detach().cpu().contiguous()
+    if x.dtype == torch.float32:
+        return x.numpy(), orc.F32
+    return orc.bf16_bits(x), (orc.BF16 if x.dtype == torch.bfloat16 else orc.F16)
+
+
+def _np(t):
+    return None if t is None else t.detach().cpu().numpy()
+
+
+def check_sampling(lsg, orc, logits, T, K, P, U, max_amb_frac=0.01):
+    ids = lsg.sample_rows(logits, T, K, P, U).cpu().numpy()
+    arr, code = _host(orc, logits)
+    ref, amb = orc.sample(arr, _np(T), _np(K), _np(P), _np(U), dtype=code)
+    bad = np.nonzero((ids != ref) & (amb == 0))[0]
+    assert bad.size == 0, f"{bad.size} mismatching rows, e.g. row {bad[:5]}: gpu {ids[bad[:5]]} oracle {ref[bad[:5]]}"
+    assert (amb != 0).mean() <= max_amb_frac, f"too many ambiguous rows: {(amb != 0).sum()}"
+    assert ((ids >= 0) & (ids < logits.shape[1])).all()
+    return ids, ref, amb
+
+
+# ------------------------------------------------------------------ greedy ----
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [1, 7, 4096, 49152, 65536, 65537, 131072, 300001])
+def test_greedy_bit_exact(lsg, orc, dev, dtype, V):
+    g = torch.Generator(device=dev).manual_seed(V)
+    B = 16
+    x = torch.randn(B, V, generator=g, device=dev).to(dtype)
+    if V > 10:
+        x[0, V // 3] = float("nan")
+        x[1, :] = 0.0
+        x[1, V // 2] = -0.0
+        x[2, V - 1] = float("inf")
+        x[3, :] = float("-inf")
+        x[4, :] = float("nan")
+        x[5, 3] = 9.0
+        x[5, V - 2] = 9.0
+        x[6, :] = 1.0
+        x[7, V - 1] = float("inf")
+        x[7, 1] = float("nan")
+    ids = lsg.sample_rows(x, None, None, None, None).cpu().numpy()
+    want = torch.argmax(x, dim=-1).to(torch.int32).cpu().numpy()  # the reference's call
+    assert np.array_equal(ids, want)
+    arr, code = _host(orc, x)
+    assert np.array_equal(ids, orc.argmax(arr, dtype=code))
+
+
+def test_greedy_sampler_interface(lsg, dev):
+    """Sampler.sample with temperatures None is argmax (sample.py:110-111)."""
+    x = torch.randn(32, 5000, device=dev)
+    s = lsg.Sampler(dev, 5000)
+    ids = s.sample(x, lsg.BatchSamplingArgs(None))
+    assert ids.dtype == torch.int32
+    assert torch.equal(ids.long(), torch.argmax(x, -1))
+
+
+# ---------------------------------------------------------------- workloads --
+def test_sample_small_golden(lsg, orc, dev):
+    """B=8, V=49152 fp32: greedy equals torch.argmax's committed ids; sampled
+    ids (T=0.7, k=50, p=0.9) equal the committed oracle ids."""
+    with open(os.path.join(HERE, "golden", "sample_small.json")) as f:
+        gold = json.load(f)
+    wl = lsg.workloads.sample_small(dev, seed=gold["seed"])
+    assert abs(float(wl["logits"].double().sum()) - gold["logits_checksum"]) < 1e-6
+    ids = lsg.sample_rows(wl["logits"], None, None, None, None).cpu().tolist()
+    assert ids == gold["greedy_ids"]
+    ids = lsg.sample_rows(wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+    ids = ids.cpu().numpy()
+    amb = np.array(gold["sampled_amb"])
+    assert np.array_equal(ids[amb == 0], np.array(gold["sampled_ids"])[amb == 0])
+
+
+def test_sample_ouro_mixed(lsg, orc, dev):
+    """B=256, V=49152 bf16 logits = h W^T; per-row T, k in {1,20,50,off}, p~U[0.8,1]."""
+    wl = lsg.workloads.sample_ouro(dev)
+    check_sampling(lsg, orc, wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+
+
+def test_sample_huginn_full(lsg, orc, dev):
+    """B=1024, V=65536 bf16 Zipf-like, T=0.6, p=0.95 (the headline workload)."""
+    wl = lsg.workloads.sample_huginn(dev)
+    check_sampling(lsg, orc, wl["logits"], wl["temperatures"], None, wl["top_p"], wl["uniforms"])
+
+
+def test_sample_mixed_depth_fp32(lsg, orc, dev):
+    """B=2048, V=65536 fp32 Student-t with exact top-2 ties; mixed greedy
+    (T=1e-6)/top-k/top-p rows."""
+    wl = lsg.workloads.cdb_mixed_depth(dev)
+    ids, ref, amb = check_sampling(lsg, orc, wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"],
+                                   wl["uniforms"], max_amb_frac=0.05)
+    # greedy rows with tied maxima split their mass: the uniform decides the tie
+    tie = wl["tie_rows"].cpu().numpy() & (wl["temperatures"].cpu().numpy() < 1e-5)
+    if tie.any():
+        top = torch.topk(wl["logits"][torch.from_numpy(tie).to(dev)], 2, dim=1).indices.sort(dim=1).values
+        top = top.cpu().numpy()
+        u = wl["uniforms"].cpu().numpy()[tie]
+        want = np.where(u < 0.5, top[:, 0], top[:, 1])
+        assert np.array_equal(ids[tie], want)
+
+
+# --------------------------------------------------------------- edge cases --
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [1, 3, 100, 1000, 8191, 40000, 65536, 150001])
+def test_modes_ragged(lsg, orc, dev, dtype, V):
+    """Every filter combination on ragged V (partial tail chunks)."""
+    g = torch.Generator(device=dev).manual_seed(1000 + V)
+    B = 24
+    x = (torch.randn(B, V, generator=g, device=dev) * 2).to(dtype)
+    T = 0.4 + torch.rand(B, generator=g, device=dev)
+    K = torch.tensor([0, 1, 5, 50, V, V + 3, -1, 2] * 3, dtype=torch.int32, device=dev)
+    P = torch.tensor([1.0, 0.9, 0.5, 1.0, 0.99, 0.3, 0.95, 1.0] * 3, device=dev)
+    U = torch.rand(B, generator=g, device=dev)
+    check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.2)
+    check_sampling(lsg, orc, x, T, None, None, U, max_amb_frac=0.2)
+    check_sampling(lsg, orc, x, T, K, None, U, max_amb_frac=0.2)
+    check_sampling(lsg, orc, x, T, None, P, U, max_amb_frac=0.2)
+
+
+def test_flat_rows_exact_path(lsg, orc, dev):
+    """Near-uniform rows make the top-p set large: the exact (bisection) path."""
+    g = torch.Generator(device=dev).manual_seed(9)
+    B, V = 16, 49152
+    x = (torch.randn(B, V, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    T = torch.full((B,), 1.0, device=dev)
+    P = torch.linspace(0.1, 0.99, B, device=dev)
+    K = torch.tensor([-1] * 8 + [30000] * 8, dtype=torch.int32, device=dev)
+    U = torch.rand(B, generator=g, device=dev)
+    check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.2)
+
+
+def test_closed_forms_gpu(lsg, dev):
+    """Uniform row -> floor(u V); one-hot -> hot index; T <= 0 -> argmax;
+    all -inf -> 0; +inf max -> first +inf (argmax rule)."""
+    V = 1000
+    u = torch.tensor([0.1234, 0.5001, 0.9999, 0.0], device=dev)
+    x = torch.zeros(4, V, device=dev)
+    ids = lsg.sample_rows(x, torch.full((4,), 0.8, device=dev), None, None, u).cpu()
+    assert ids.tolist() == [123, 500, 999, 0]
+    x = torch.full((4, V), -1000.0, device=dev)
+    x[:, 321] = 30.0
+    assert lsg.sample_rows(x, torch.ones(4, device=dev), None, None, u).cpu().tolist() == [321] * 4
+    y = torch.randn(4, V, device=dev)
+    y[2, :] = float("-inf")
+    y[3, 7] = float("inf")
+    y[3, 9] = float("inf")
+    ids = lsg.sample_rows(y, torch.tensor([0.0, -1.0, 1.0, 1.0], device=dev), None, None, u).cpu()
+    assert ids[0] == torch.argmax(y[0]).item() and ids[1] == torch.argmax(y[1]).item()
+    assert ids[2] == 0 and ids[3] == 7
+
+
+def test_nan_logits_in_sampling_rows(lsg, orc, dev):
+    """NaN logits carry no mass in sampling rows (treated as -inf)."""
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(8, 3000, generator=g, device=dev)
+    x[:, ::7] = float("nan")
+    T = torch.full((8,), 0.9, device=dev)
+    U = torch.rand(8, generator=g, device=dev)
+    ids, _, _ = check_sampling(lsg, orc, x, T, torch.full((8,), 20, dtype=torch.int32, device=dev),
+                               torch.full((8,), 0.8, device=dev), U)
+    assert (ids % 7 != 0).all()
+
+
+def test_unaligned_rows(lsg, orc, dev):
+    """Row stride not a multiple of 16 bytes and an odd base offset."""
+    g = torch.Generator(device=dev).manual_seed(6)
+    big = torch.randn(12, 50258, generator=g, device=dev).to(torch.bfloat16)
+    x = big[:, 1:50258]  # V = 50257 (GPT-2 vocab), ld = 50258, base offset 2 bytes
+    T = torch.full((12,), 0.8, device=dev)
+    U = torch.rand(12, generator=g, device=dev)
+    check_sampling(lsg, orc, x.contiguous(), T, None, torch.full((12,), 0.9, device=dev), U)
+    ids_view = lsg.sample_rows(x, T, None, torch.full((12,), 0.9, device=dev), U)
+    ids_cont = lsg.sample_rows(x.contiguous(), T, None, torch.full((12,), 0.9, device=dev), U)
+    assert torch.equal(ids_view, ids_cont)
+    assert torch.equal(lsg.sample_rows(x, None, None, None, None).long(), torch.argmax(x, -1))
+
+
+def test_gather_and_device_count(lsg, dev):
+    """row_idx gathers rows (invalid -> -1); n_rows limits the rows written."""
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(10, 4096, generator=g, device=dev)
+    idx = torch.tensor([9, 0, 3, 42, -1, 5], dtype=torch.int32, device=dev)
+    out = torch.full((6,), -7, dtype=torch.int32, device=dev)
+    lsg.sample_rows(x, None, None, None, None, row_idx=idx, out=out)
+    am = torch.argmax(x, -1)
+    assert out.cpu().tolist() == [am[9].item(), am[0].item(), am[3].item(), -1, -1, am[5].item()]
+    out.fill_(-7)
+    n = torch.tensor([2], dtype=torch.int32, device=dev)
+    T = torch.full((10,), 0.7, device=dev)
+    U = torch.rand(10, generator=g, device=dev)
+    lsg.sample_rows(x, T, None, None, U, row_idx=idx, n_rows=n, out=out)
+    full = lsg.sample_rows(x, T, None, None, U)
+    got = out.cpu().tolist()
+    assert got[:2] == [full[9].item(), full[0].item()] and got[2:] == [-7] * 4
+
+
+def test_deterministic(lsg, dev):
+    wl = lsg.workloads.sample_ouro(dev)
+    a = lsg.sample_rows(wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+    b = lsg.sample_rows(wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+    assert torch.equal(a, b)
+
+
+def test_graph_replay(lsg, dev):
+    """Captured in a HIP graph, every replay matches eager execution."""
+    wl = lsg.workloads.sample_ouro(dev, B=64)
+    args = (wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+    eager = lsg.sample_rows(*args).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lsg.sample_rows(*args)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = lsg.sample_rows(*args)
+    for i in range(3):
+        out.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+    wl["uniforms"].copy_(torch.rand_like(wl["uniforms"]))
+    graph.replay()
+    assert torch.equal(out, lsg.sample_rows(*args))
+
+
+def test_sampler_prepare_and_sample(lsg, orc, dev):
+    """Sampler.prepare normalises per-request params; sample draws with the
+    given uniforms (greedy rows in a mixed batch use T=1e-6)."""
+    from types import SimpleNamespace
+
+    SP = lsg.SamplingParams
+    reqs = [SimpleNamespace(sampling_params=p) for p in
+            [SP(), SP(temperature=0.8, top_k=20), SP(temperature=1.0, top_p=0.9), SP(top_k=1, temperature=2.0)]]
+    s = lsg.Sampler(dev, 3000)
+    args = s.prepare(SimpleNamespace(reqs=reqs))
+    assert args.temperatures is not None
+    x = torch.randn(4, 3000, device=dev)
+    args.uniforms = torch.rand(4, device=dev)
+    ids = s.sample(x, args)
+    check_sampling(lsg, orc, x, args.temperatures, args.top_k, args.top_p, args.uniforms)
+    # rows 0 and 3 are greedy: T = 1e-6 puts all mass on the argmax
+    am = torch.argmax(x, -1)
+    assert ids[0].item() == am[0].item() and ids[3].item() == am[3].item()
+    # without uniforms the sampler draws its own (seeded) ones
+    args.uniforms = None
+    a = s.sample(x, args)
+    assert ((a >= 0) & (a < 3000)).all()
