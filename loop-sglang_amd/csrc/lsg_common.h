@@ -134,6 +134,14 @@ __device__ __forceinline__ float chunk_max(const uint4& v) {
   return m;
 }
 
+template <typename T>
+__device__ __forceinline__ float chunk_maximum(const uint4& v) {
+  float m = Elem<T>::get(v, 0);
+#pragma unroll
+  for (int i = 1; i < Elem<T>::EPV; ++i) m = __builtin_elementwise_maximum(m, Elem<T>::get(v, i));
+  return m;
+}
+
 // ---------------------------------------------------------------------------
 // Move a wave-uniform value into scalar registers (frees a VGPR; the value must
 // be identical in every active lane).
@@ -153,56 +161,117 @@ __device__ __forceinline__ double uni(double v) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave reductions (xor butterfly: every lane ends with the identical value).
+// DPP cross-lane helpers (GFX9 wave64).  dpp<CTRL, ROWMASK>(old, v): lanes in
+// enabled rows read lane CTRL(i) of v; lanes whose source is invalid or whose
+// row is disabled keep `old`.
+//   row_shr:n = 0x110+n, row_ror:n = 0x120+n, row_bcast15 = 0x142,
+//   row_bcast31 = 0x143.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWMASK, 0xf, false);
 }
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __int_as_float(dpp_i<CTRL, ROWMASK>(__float_as_int(old), __float_as_int(v)));
 }
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ double dpp_d(double old, double v) {
+  const long long o = __double_as_longlong(old), x = __double_as_longlong(v);
+  const int lo = dpp_i<CTRL, ROWMASK>((int)(o & 0xffffffffll), (int)(x & 0xffffffffll));
+  const int hi = dpp_i<CTRL, ROWMASK>((int)(o >> 32), (int)(x >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
-  return v;
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
-__device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
-  return v;
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Inclusive prefix sum across the wave (Hillis-Steele, fixed order).
-__device__ __forceinline__ double wave_incl_scan(double v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const double u = __shfl_up(v, o);
-    if (lane >= o) v += u;
-  }
+// Wave reductions.  Rows of 16 lanes are reduced with row_ror butterflies,
+// then the four row results (lanes 0, 16, 32, 48) are combined in a fixed
+// order in scalar registers: the result is deterministic and wave-uniform.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0x128>(v, v));
+  v = fmaxf(v, dpp_f<0x124>(v, v));
+  v = fmaxf(v, dpp_f<0x122>(v, v));
+  v = fmaxf(v, dpp_f<0x121>(v, v));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+// NaN-propagating maximum (IEEE 754-2019 maximum; v_maximum3_f32 on gfx950).
+__device__ __forceinline__ float fmaximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float wave_maximum(float v) {
+  v = fmaximum(v, dpp_f<0x128>(v, v));
+  v = fmaximum(v, dpp_f<0x124>(v, v));
+  v = fmaximum(v, dpp_f<0x122>(v, v));
+  v = fmaximum(v, dpp_f<0x121>(v, v));
+  return fmaximum(fmaximum(readlane_f(v, 0), readlane_f(v, 16)),
+                  fmaximum(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ double wave_sum(double v) {
+  v += dpp_d<0x128>(0.0, v);
+  v += dpp_d<0x124>(0.0, v);
+  v += dpp_d<0x122>(0.0, v);
+  v += dpp_d<0x121>(0.0, v);
+  return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += dpp_i<0x128>(0, v);
+  v += dpp_i<0x124>(0, v);
+  v += dpp_i<0x122>(0, v);
+  v += dpp_i<0x121>(0, v);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, dpp_i<0x128>(v, v));
+  v = min(v, dpp_i<0x124>(v, v));
+  v = min(v, dpp_i<0x122>(v, v));
+  v = min(v, dpp_i<0x121>(v, v));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, dpp_i<0x128>(v, v));
+  v = max(v, dpp_i<0x124>(v, v));
+  v = max(v, dpp_i<0x122>(v, v));
+  v = max(v, dpp_i<0x121>(v, v));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Inclusive prefix sum across the wave in lane order: row_shr 1/2/4/8 inside
+// each row of 16, then row_bcast15 / row_bcast31 carry row totals forward.
+__device__ __forceinline__ double wave_incl_scan(double v, int /*lane*/) {
+  v += dpp_d<0x111>(0.0, v);
+  v += dpp_d<0x112>(0.0, v);
+  v += dpp_d<0x114>(0.0, v);
+  v += dpp_d<0x118>(0.0, v);
+  v += dpp_d<0x142, 0xa>(0.0, v);
+  v += dpp_d<0x143, 0xc>(0.0, v);
   return v;
 }
-__device__ __forceinline__ int wave_incl_scan_i(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o);
-    if (lane >= o) v += u;
-  }
+__device__ __forceinline__ int wave_incl_scan_i(int v, int /*lane*/) {
+  v += dpp_i<0x111>(0, v);
+  v += dpp_i<0x112>(0, v);
+  v += dpp_i<0x114>(0, v);
+  v += dpp_i<0x118>(0, v);
+  v += dpp_i<0x142, 0xa>(0, v);
+  v += dpp_i<0x143, 0xc>(0, v);
   return v;
 }
+// Value of lane i-1 (0 in lane 0): wave_shr:1.
+__device__ __forceinline__ double wave_shr1(double v) { return dpp_d<0x138>(0.0, v); }
 
 // ---------------------------------------------------------------------------
 // Workgroup reductions.  `red` is a __shared__ scratch area of at least NW
-// elements of 8 bytes.  Every thread returns the identical value.  Each call
-// ends with a barrier, so the scratch can be reused immediately.
+// elements of 8 bytes.  Wave results (already wave-uniform) are combined in
+// wave order, so every thread returns the identical value.  Each call ends with
+// a barrier, so the scratch can be reused immediately.
 // ---------------------------------------------------------------------------
 template <int NW>
 __device__ __forceinline__ float wg_max(float v, double* red) {
@@ -213,6 +282,18 @@ __device__ __forceinline__ float wg_max(float v, double* red) {
   float r = reinterpret_cast<float*>(red)[0];
 #pragma unroll
   for (int i = 1; i < NW; ++i) r = fmaxf(r, reinterpret_cast<float*>(red)[i]);
+  __syncthreads();
+  return uni(r);
+}
+template <int NW>
+__device__ __forceinline__ float wg_maximum(float v, double* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_maximum(v);
+  if (lane == 0) reinterpret_cast<float*>(red)[w] = v;
+  __syncthreads();
+  float r = reinterpret_cast<float*>(red)[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r = fmaximum(r, reinterpret_cast<float*>(red)[i]);
   __syncthreads();
   return uni(r);
 }
@@ -272,8 +353,7 @@ template <int NW>
 __device__ __forceinline__ double wg_scan(double v, double* red, double* incl, double* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const double wi = wave_incl_scan(v, lane);
-  double we = __shfl_up(wi, 1);
-  if (lane == 0) we = 0.0;
+  const double we = wave_shr1(wi);
   if (lane == 63) red[w] = wi;
   __syncthreads();
   // base(w) is the running sum of the preceding wave totals in index order, so

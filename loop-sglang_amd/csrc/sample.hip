@@ -6,12 +6,15 @@
 //   torch.argmax (greedy)     sample.py:110-111 (+ int32 cast, model_runner.py:279-280)
 //   sample_impl -> flashinfer softmax / *_sampling_from_probs   sample.py:60-81
 //
-// One workgroup samples one row.  The row is read from HBM exactly once with
-// coalesced 128-bit loads (wave w owns a contiguous span of the row and reads
-// it 1 KiB per instruction) and stays in VGPRs (CAP chunks of 16 B per
-// thread); the later passes (softmax normaliser, threshold search, CDF walk)
-// run on registers and LDS.  Chunks past NT*CAP (very large V), and the rare
-// exact slow path of the threshold search, re-read the row from global memory.
+// One workgroup samples one row at a time.  The row is read from HBM exactly
+// once with coalesced 128-bit loads (wave w owns a contiguous span of the row
+// and reads it 1 KiB per instruction) and stays in VGPRs (CAP chunks of 16 B
+// per thread); the later passes (softmax normaliser, threshold search, CDF
+// walk) run on registers and LDS.  For rows that fit twice in the register
+// budget the kernel is persistent and double-buffered: while a workgroup works
+// on one row, the loads of its next row are already in flight, so HBM streams
+// continuously.  Chunks past NT*CAP (very large V), and the rare exact slow
+// path of the threshold search, re-read the row from global memory.
 //
 // Semantics (per row r, x = float32(logit), NaN treated as -inf):
 //   T <= 0 or non-finite, or max x non-finite  -> id = argmax (torch rules)
@@ -25,17 +28,17 @@
 #include "lsg_capi_internal.h"
 #include "lsg_common.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace lsg {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBins = 64;   // thread-maximum histogram: bins of width 1 in log2 units
-constexpr int kLMax = 64;   // max chunk loads per thread (V <= kLMax * NT * EPV)
 
 struct SampleParams {
   const void* logits;
-  int64_t B_src, V, ld;
+  int64_t B_src, V, ld, B_out;
   const float* temps;
   const int32_t* top_k;
   const float* top_p;
@@ -103,7 +106,7 @@ struct RowBase {
   uint32_t c0;  // chunk index of this thread's j = 0 load
   __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, int64_t Vv) {
     base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)Elem<T>::kSize;
-    V = (uint32_t)Vv;
+    V = (uint32_t)uni((uint32_t)Vv);
     const uint32_t NV = (V + EPV - 1) / EPV;
     L = (int)((NV + NT - 1) / NT);
     c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)L * kWave + (threadIdx.x & 63);
@@ -164,6 +167,17 @@ struct RegRow : RowBase<T, NT, VEC> {
     for (int j = 0; j < CAP; ++j)
       if (j < B::L) d[j] = B::load(j);
   }
+  // Registers from a row staged in LDS (chunk c at s_row[c]); partial and
+  // padding chunks, which the staging loads skipped, come from global memory.
+  __device__ __forceinline__ void fetch_staged(const uint4* s_row) {
+    constexpr int EPV = Elem<T>::EPV;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (j < B::L) {
+        const uint32_t c = B::chunk_index(j);
+        d[j] = (c * EPV + EPV <= B::V) ? s_row[c] : B::load(j);
+      }
+  }
   // Tell the compiler the register copy may have changed, so values derived
   // from it (unpacked floats) are recomputed per pass instead of being hoisted
   // and kept live across passes (which would double the register footprint).
@@ -217,6 +231,21 @@ struct MemRow : RowBase<T, NT, VEC> {
   __device__ __forceinline__ uint4 chunk(int j) const { return B::load(j); }
 };
 
+// LDS shared by the per-row routines (one row at a time per workgroup).
+template <int NT>
+struct Smem {
+  static constexpr int NW = NT / kWave;
+  static constexpr int kWin = NT < 512 ? NT : 512;  // candidate window capacity
+  double red[NW];
+  double col[NW];
+  int hcnt[kBins];
+  float hmass[kBins];
+  uint64_t wkey[kWin];    // candidate window (unsorted)
+  uint64_t sorted[kWin];  // candidate window in descending key order
+  int wn;
+  int pick;
+};
+
 // argmax with torch semantics.  gm is the NaN-ignoring maximum, tm this
 // thread's.  Returns the id (identical in every thread).
 template <int NW, typename T, class Row>
@@ -241,15 +270,6 @@ __device__ __forceinline__ int32_t row_argmax(Row& R, float tm, float gm, double
     });
   }
   return wg_min_i<NW>(first, red);
-}
-
-// Resolve the output row b -> source row r; -1: skip the row, -2: invalid
-// gather index (the output gets -1).
-__device__ __forceinline__ int64_t resolve_row(const SampleParams& P, int b) {
-  if (P.n_rows_dev && b >= *P.n_rows_dev) return -1;
-  const int64_t r = P.row_idx ? (int64_t)P.row_idx[b] : (int64_t)b;
-  if (r < 0 || r >= P.B_src) return -2;
-  return r;
 }
 
 // ---------------------------------------------------------------------------
@@ -302,41 +322,30 @@ __device__ float select_exact(Row& R, float gm, float c, double Z, bool kon, int
 // Inverse CDF in ascending index order over {x >= thr} (all when !masked).
 // Index order is (wave, j, lane, element): find the wave whose prefix crosses
 // U = u * total, then (inside that wave only) the column j, then the lane,
-// then the element.  Every level reuses the same chunk masses summed in a
-// fixed order, so the walk is deterministic.  s_cs[j*NT + t] holds the chunk
-// masses for j < CAP (filled here unless cs_valid).
+// then the element.  The wave that holds the crossing recomputes its chunk
+// masses with the same arithmetic that produced the totals, so every level
+// sees identical values and the walk is deterministic.  tmass is this
+// thread's mass (all its chunks, masked like the walk).
 // ---------------------------------------------------------------------------
-template <int NT, int CAP, typename T, class Row>
+template <int NT, typename T, class Row>
 __device__ __forceinline__ void cdf_pick(Row& R, float gm, float c, bool masked, float thr,
-                                         bool cs_valid, double tmass_valid, float u, float* s_cs,
-                                         double* s_col, int32_t* out) {
+                                         double tmass, float u, Smem<NT>& S, int32_t* out) {
   constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  double tmass = tmass_valid;
-  if (!cs_valid) {
-    tmass = 0.0;
-    R.each([&](int j, const uint4& v, float cmj) {
-      const float s = masked ? (cmj >= thr ? esum_chunk_ge<T>(v, gm, c, thr) : 0.0f)
-                             : esum_chunk<T>(v, gm, c);
-      if (j < CAP) s_cs[j * NT + t] = s;
-      tmass += (double)s;
-    });
-  }
   {
     const double ws = wave_sum(tmass);
-    if (lane == 0) s_col[wid] = ws;
+    if (lane == 0) S.col[wid] = ws;
   }
   __syncthreads();
-  // Wave totals in index order: lane w of every wave holds wave w's total and
-  // a wave scan gives the prefixes (identical in every wave).
+  // Wave totals in index order: lane w of every wave holds wave w's total and a
+  // wave scan gives the prefixes (identical in every wave).
   int wstar;
   double base, U;
   {
-    const double sw = lane < NW ? s_col[lane] : 0.0;
+    const double sw = lane < NW ? S.col[lane] : 0.0;
     const double inc = wave_incl_scan(sw, lane);
-    const double total = uni(__shfl(inc, NW - 1));
+    const double total = readlane_d(inc, NW - 1);
     U = (double)u * total;
-    const double exc = inc - sw;  // only compared, never accumulated further
     const uint64_t cross = __ballot(lane < NW && inc > U);
     if (cross) {
       wstar = __ffsll((unsigned long long)cross) - 1;
@@ -344,41 +353,40 @@ __device__ __forceinline__ void cdf_pick(Row& R, float gm, float c, bool masked,
       const uint64_t pos = __ballot(lane < NW && sw > 0.0);
       wstar = pos ? 63 - __clzll((long long)pos) : 0;
     }
-    (void)exc;
-    double ex = __shfl_up(inc, 1);
-    if (lane == 0) ex = 0.0;
-    base = uni(__shfl(ex, wstar));
+    wstar = uni(wstar);
+    base = readlane_d(wave_shr1(inc), wstar);
   }
   if (wid != wstar) return;
-  auto colmass = [&](int j) -> float {
-    if (j < CAP) return s_cs[j * NT + t];
-    const uint4 v = R.chunk(j);
-    return masked ? esum_chunk_ge<T>(v, gm, c, thr) : esum_chunk<T>(v, gm, c);
-  };
-  // column j inside the wave (sequential; one column mass at a time)
+  // column j inside the wave: one pass over this wave's chunks in index order
   int jstar = -1, jlast = 0;
-  double jbase = base, cum = base;
-  for (int j = 0; j < R.L; ++j) {
-    const double col = wave_sum((double)colmass(j));
-    if (col > 0.0) jlast = j;
+  double jbase = base, cum = base, cum_last = base;
+  float sme = 0.0f, slast = 0.0f;
+  R.each([&](int j, const uint4& v, float cmj) {
+    const float sj = masked ? (cmj >= thr ? esum_chunk_ge<T>(v, gm, c, thr) : 0.0f)
+                            : esum_chunk<T>(v, gm, c);
+    const double col = wave_sum((double)sj);
+    if (col > 0.0) {
+      jlast = j;
+      slast = sj;
+      cum_last = cum;
+    }
     if (jstar < 0 && cum + col > U) {
       jstar = j;
       jbase = cum;
+      sme = sj;
     }
     cum += col;
-  }
-  if (jstar < 0) {
+  });
+  if (jstar < 0) {  // u >= 1 or rounding: the last column with mass
     jstar = jlast;
-    jbase = base;
-    for (int j = 0; j < jlast; ++j) jbase += wave_sum((double)colmass(j));
+    jbase = cum_last;
+    sme = slast;
   }
+  jstar = uni(jstar);
   // lane inside the column
-  const float sme = colmass(jstar);
   const double incl = wave_incl_scan((double)sme, lane);
-  double excl = __shfl_up(incl, 1);
-  if (lane == 0) excl = 0.0;
-  const bool cross = (sme > 0.0f) && (jbase + excl <= U) && (jbase + incl > U);
-  const uint64_t bal = __ballot(cross);
+  const double excl = wave_shr1(incl);
+  const uint64_t bal = __ballot((sme > 0.0f) && (jbase + incl > U));
   int owner;
   if (bal) {
     owner = __ffsll((unsigned long long)bal) - 1;
@@ -386,8 +394,8 @@ __device__ __forceinline__ void cdf_pick(Row& R, float gm, float c, bool masked,
     const uint64_t pos = __ballot(sme > 0.0f);
     owner = pos ? 63 - __clzll((long long)pos) : 0;
   }
+  const uint4 vj = R.chunk(jstar);
   if (lane == owner) {
-    const uint4 vj = R.chunk(jstar);
     double acc = jbase + excl;
     int pick = -1, lastpos = -1;
 #pragma unroll
@@ -406,68 +414,128 @@ __device__ __forceinline__ void cdf_pick(Row& R, float gm, float c, bool masked,
 }
 
 // ---------------------------------------------------------------------------
-// Greedy kernel: every row is argmax (Sampler.sample with temperatures None).
+// Candidate window bounded by a histogram of distinct elements (the thread
+// maxima, or the chunk maxima): since they are distinct elements, the window
+// {y >= lo} holds >= k elements once >= k of them have y >= lo, and holds mass
+// >= p*Z once those with y >= lo carry that much mass.  Returns the bin b (the
+// window is y >= -(b+1)) or -1 when no bin reaches the target.
 // ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC>
-__global__ __launch_bounds__(NT) void greedy_kernel(SampleParams P) {
-  constexpr int NW = NT / kWave;
-  __shared__ double red[NW];
-  const int b = blockIdx.x;
-  const int64_t r = resolve_row(P, b);
-  if (r == -1) return;
-  if (r == -2) {
-    if (threadIdx.x == 0) P.out[b] = -1;
-    return;
+template <int NT>
+__device__ __forceinline__ int window_bin(Smem<NT>& S, bool kon, int32_t k, float p, double Z) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (wid == 0) {
+    const int pc = wave_incl_scan_i(S.hcnt[lane], lane);
+    const double pm = wave_incl_scan((double)S.hmass[lane], lane);
+    const bool ok = kon ? (pc >= k) : (pm >= (double)p * Z);
+    const uint64_t bal = __ballot(ok);
+    if (lane == 0) S.pick = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
   }
-  RegRow<T, NT, CAP, VEC> R;
-  R.init(P.logits, r, P.ld, P.V);
-  R.fetch();
-  float tm = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < CAP; ++j)
-    if (j < R.L) {
-      const float m = chunk_max<T>(R.d[j]);
-      R.cm.set(j, m);
-      tm = fmaxf(tm, m);
-    }
-  for (int j = CAP; j < R.L; ++j) tm = fmaxf(tm, chunk_max<T>(R.load(j)));
-  const float gm = wg_max<NW>(tm, red);
-  const int32_t id = row_argmax<NW, T>(R, tm, gm, red);
-  if (threadIdx.x == 0) P.out[b] = id;
+  __syncthreads();
+  const int bin = uni(S.pick);
+  __syncthreads();
+  return bin;
+}
+
+__device__ __forceinline__ int ybin(float y) { return min(kBins - 1, (int)(-y)); }
+
+// ---------------------------------------------------------------------------
+// One sampling row: row r of the logits -> out[b].  Every path is uniform
+// across the workgroup (all threads reach the same barriers).
+// ---------------------------------------------------------------------------
+struct RowArgs {
+  float T, p, u;
+  int32_t k;
+};
+
+__device__ __forceinline__ RowArgs row_args(const SampleParams& P, int64_t r) {
+  RowArgs a;
+  a.T = P.temps ? uni(P.temps[r]) : 0.0f;
+  a.u = P.uniforms ? uni(P.uniforms[r]) : 0.0f;
+  a.k = uni(P.top_k ? P.top_k[r] : 0);
+  a.p = uni(P.top_p ? P.top_p[r] : 1.0f);
+  return a;
 }
 
 // ---------------------------------------------------------------------------
-// Sampling kernel.
+// Rare rows, outside the hot path's register allocation: they re-read the row
+// from global memory.
+//   mode 0: argmax (T <= 0, or a non-finite maximum, inside a sampling batch)
+//   mode 1: exact top-k / top-p threshold, then the masked CDF walk
 // ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8)))
-void sample_kernel(SampleParams P) {
-  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
-  constexpr int kWin = NT;  // candidate window: one entry per thread
-  __shared__ double red[NW];
-  __shared__ double s_col[NW];
-  __shared__ float s_cs[CAP * NT];  // chunk masses, [j][t]
-  __shared__ int s_hcnt[kBins];
-  __shared__ float s_hmass[kBins];
-  __shared__ uint64_t s_wkey[kWin];
-  __shared__ uint64_t s_sorted[kWin];
-  __shared__ int s_wn;
-  __shared__ int s_pick;
-
-  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  const int b = blockIdx.x;
-  const int64_t r = resolve_row(P, b);
-  if (r == -1) return;
-  if (r == -2) {
-    if (t == 0) P.out[b] = -1;
+template <typename T, int NT, bool VEC>
+__device__ __attribute__((noinline)) void rare_row(const void* logits, int64_t r, int64_t ld,
+                                                   int64_t V, int mode, float tm, float gm, float c,
+                                                   double Z, int32_t k, float p, float u,
+                                                   Smem<NT>* Sp, int32_t* out) {
+  constexpr int NW = NT / kWave;
+  Smem<NT>& S = *Sp;
+  MemRow<T, NT, VEC> M;
+  M.init(logits, r, ld, V);
+  if (mode == 0) {
+    const int32_t id = row_argmax<NW, T>(M, tm, gm, S.red);
+    if (threadIdx.x == 0) *out = id;
     return;
   }
+  const bool kon = k >= 1 && (int64_t)k < V, pon = p < 1.0f;
+  const float thr = select_exact<NW, T>(M, gm, c, Z, kon, k, pon, p, S.red);
+  double tmass = 0.0;
+  M.each([&](int, const uint4& v, float cmj) {
+    if (cmj >= thr) tmass += (double)esum_chunk_ge<T>(v, gm, c, thr);
+  });
+  cdf_pick<NT, T>(M, gm, c, true, thr, tmass, u, S, out);
+}
 
-  RegRow<T, NT, CAP, VEC> R;
-  R.init(P.logits, r, P.ld, P.V);
-  R.fetch();
+// ---------------------------------------------------------------------------
+// Greedy row: torch.argmax.  NaN-propagating maxima make a NaN anywhere the
+// row maximum, so one pass finds both the maximum and whether NaN is present;
+// the chunk maxima then point at the single chunk holding the first hit.
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int CAP, bool VEC>
+__device__ __forceinline__ void greedy_row(RegRow<T, NT, CAP, VEC>& R, int32_t* out, Smem<NT>& S) {
+  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
+  __syncthreads();
+  float tm = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j)
+    if (j < R.L) {
+      const float m = chunk_maximum<T>(R.d[j]);
+      R.cm.set(j, m);
+      tm = fmaximum(tm, m);
+    }
+  for (int j = CAP; j < R.L; ++j) tm = fmaximum(tm, chunk_maximum<T>(R.load(j)));
+  const float gm = wg_maximum<NW>(tm, S.red);
+  const bool isn = gm != gm;
+  int first = 0x7fffffff;
+  if (isn ? (tm != tm) : (tm == gm)) {
+    R.each([&](int j, const uint4& v, float cmj) {
+      if (first == 0x7fffffff && (j >= CAP || (isn ? cmj != cmj : cmj == gm))) {
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+          const float x = Elem<T>::get(v, i);
+          const uint32_t idx = R.elem_index(j, i);
+          if (first == 0x7fffffff && (isn ? x != x : x == gm) && idx < R.V) first = (int)idx;
+        }
+      }
+    });
+  }
+  const int32_t id = wg_min_i<NW>(first, S.red);
+  if (threadIdx.x == 0) *out = id;
+}
 
-  // ---- pass A: chunk maxima and the row maximum --------------------------
+// ---------------------------------------------------------------------------
+// One sampling row: row r of the logits -> *out.  Every path is uniform across
+// the workgroup (all threads reach the same barriers).
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int CAP, bool VEC>
+__device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const SampleParams& P,
+                                           int64_t r, const RowArgs& A, int32_t* out, Smem<NT>& S) {
+  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
+  constexpr int kWin = Smem<NT>::kWin;
+  const int t = threadIdx.x, wid = t >> 6;
+  __syncthreads();  // the previous row's readers of S are done
+
+  // ---- pass A: chunk maxima and the row maximum (NaN ignored) ------------
   float tm = -INFINITY;
 #pragma unroll
   for (int j = 0; j < CAP; ++j)
@@ -477,72 +545,64 @@ void sample_kernel(SampleParams P) {
       tm = fmaxf(tm, m);
     }
   for (int j = CAP; j < R.L; ++j) tm = fmaxf(tm, chunk_max<T>(R.load(j)));
-  const float gm = wg_max<NW>(tm, red);
+  const float gm = wg_max<NW>(tm, S.red);
 
-  const float Tr = uni(P.temps[r]);
-  if (!(Tr > 0.0f) || !(Tr < INFINITY) || !(gm > -INFINITY) || !(gm < INFINITY)) {
-    // argmax rows inside a sampling batch are rare; re-read the row instead of
-    // keeping this path's registers alongside the sampling path's.
-    MemRow<T, NT, VEC> M;
-    M.init(P.logits, r, P.ld, P.V);
-    const int32_t id = row_argmax<NW, T>(M, tm, gm, red);
-    if (t == 0) P.out[b] = id;
+  if (!(A.T > 0.0f) || !(A.T < INFINITY) || !(gm > -INFINITY) || !(gm < INFINITY)) {
+    rare_row<T, NT, VEC>(P.logits, r, P.ld, P.V, 0, tm, gm, 0.0f, 0.0, 0, 1.0f, 0.0f, &S, out);
     return;
   }
-  const float c = kLog2e / Tr;
-  const float u = uni(P.uniforms[r]);
+  const float c = kLog2e / A.T;
 
-  // ---- pass B: softmax normaliser; chunk masses kept in LDS for the CDF ---
+  // ---- pass B: softmax normaliser ------------------------------------------
   R.launder();
   double zt = 0.0;
 #pragma unroll
   for (int j = 0; j < CAP; ++j)
-    if (j < R.L) {
-      const float s = esum_chunk<T>(R.d[j], gm, c);
-      s_cs[j * NT + t] = s;
-      zt += (double)s;
-    }
+    if (j < R.L) zt += (double)esum_chunk<T>(R.d[j], gm, c);
   for (int j = CAP; j < R.L; ++j) zt += (double)esum_chunk<T>(R.load(j), gm, c);
-  const double Z = wg_sum<NW>(zt, red);
+  const double Z = wg_sum<NW>(zt, S.red);
 
-  const int32_t k = uni(P.top_k ? P.top_k[r] : 0);
-  const float p = uni(P.top_p ? P.top_p[r] : 1.0f);
+  const int32_t k = A.k;
+  const float p = A.p;
   const bool kon = k >= 1 && (int64_t)k < (int64_t)R.V;
   const bool pon = p < 1.0f;
-
   if (!kon && !pon) {
-    cdf_pick<NT, CAP, T>(R, gm, c, false, -INFINITY, true, zt, u, s_cs, s_col, &P.out[b]);
+    cdf_pick<NT, T>(R, gm, c, false, -INFINITY, zt, A.u, S, out);
     return;
   }
 
-  // ---- fast path: a candidate window bounded by the thread maxima ----------
-  // Every thread maximum is a distinct element, so the window {y >= lo} holds
-  // >= k elements once >= k thread maxima have y >= lo, and holds mass >= p*Z
-  // once the thread maxima with y >= lo carry that much mass.
+  // ---- candidate window from the thread maxima, else the chunk maxima (two
+  // heavy tokens can share a thread, rarely a 16-byte chunk) ----------------
   if (t < kBins) {
-    s_hcnt[t] = 0;
-    s_hmass[t] = 0.0f;
+    S.hcnt[t] = 0;
+    S.hmass[t] = 0.0f;
   }
-  if (t == 0) s_wn = 0;
+  if (t == 0) S.wn = 0;
   __syncthreads();
   {
     const float ytm = (tm - gm) * c;
     if (ytm >= -64.0f) {
-      const int bin = min(kBins - 1, (int)(-ytm));
-      atomicAdd(&s_hcnt[bin], 1);
-      atomicAdd(&s_hmass[bin], ex2c(ytm));
+      atomicAdd(&S.hcnt[ybin(ytm)], 1);
+      atomicAdd(&S.hmass[ybin(ytm)], ex2c(ytm));
     }
   }
-  __syncthreads();
-  if (wid == 0) {
-    const int pc = wave_incl_scan_i(s_hcnt[lane], lane);
-    const double pm = wave_incl_scan((double)s_hmass[lane], lane);
-    const bool ok = kon ? (pc >= k) : (pm >= (double)p * Z);
-    const uint64_t bal = __ballot(ok);
-    if (lane == 0) s_pick = bal ? (__ffsll((unsigned long long)bal) - 1) : (kBins - 1);
+  int bin = window_bin(S, kon, k, p, Z);
+  if (bin < 0) {
+    if (t < kBins) {
+      S.hcnt[t] = 0;
+      S.hmass[t] = 0.0f;
+    }
+    __syncthreads();
+    R.each([&](int, const uint4&, float cmj) {
+      const float y = (cmj - gm) * c;
+      if (y >= -64.0f) {
+        atomicAdd(&S.hcnt[ybin(y)], 1);
+        atomicAdd(&S.hmass[ybin(y)], ex2c(y));
+      }
+    });
+    bin = window_bin(S, kon, k, p, Z);
   }
-  __syncthreads();
-  const float lo_y = -(float)(uni(s_pick) + 1);
+  const float lo_y = -(float)((bin < 0 ? kBins - 1 : bin) + 1);
 
   // collect the window (chunk maxima prune almost every chunk)
   R.each([&](int j, const uint4& v, float cmj) {
@@ -551,107 +611,262 @@ void sample_kernel(SampleParams P) {
       for (int i = 0; i < EPV; ++i) {
         const float x = Elem<T>::get(v, i);
         if ((x - gm) * c >= lo_y) {
-          const int pos = atomicAdd(&s_wn, 1);
+          const int pos = atomicAdd(&S.wn, 1);
           if (pos < kWin) {
             const uint32_t idx = R.elem_index(j, i);
-            s_wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - idx);
+            S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - idx);
           }
         }
       }
     }
   });
   __syncthreads();
-  const int nw = uni(s_wn);
+  const int nw = uni(S.wn);
   bool ok = nw <= kWin;
   float thr = -INFINITY;
-  if (ok) {
-    // rank by counting (keys are unique), scatter into descending order
-    if (t < nw) {
-      const uint64_t mine = s_wkey[t];
+  if (nw <= kWave) {
+    // Small window: wave 0 ranks, scans and thresholds it alone.
+    if (wid == 0) {
+      const int lane = t;
+      const uint64_t mine = lane < nw ? S.wkey[lane] : 0ull;
       int rank = 0;
-      for (int q = 0; q < nw; ++q) rank += s_wkey[q] > mine ? 1 : 0;
-      s_sorted[rank] = mine;
+      for (int q = 0; q < nw; ++q) {
+        const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
+        rank += other > mine ? 1 : 0;
+      }
+      if (lane < nw) S.sorted[rank] = mine;
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
+      const uint64_t key = lane < nw ? S.sorted[lane] : 0ull;
+      const uint32_t kx = (uint32_t)(key >> 32);
+      const float e = lane < nw ? ex2c((okey_inv(kx) - gm) * c) : 0.0f;
+      const double pre = wave_incl_scan((double)e, lane);  // inclusive prefix in sorted order
+      double ZK = Z;
+      int limit = nw;
+      float th = -INFINITY;
+      if (kon) {
+        const uint32_t kk = (uint32_t)__builtin_amdgcn_readlane((int)kx, (k <= nw ? k : nw) - 1);
+        limit = __popcll(__ballot(lane < nw && kx >= kk));
+        th = okey_inv(kk);
+        ZK = readlane_d(pre, limit - 1);
+      }
+      int good = 1;
+      if (pon) {
+        const uint64_t hit = __ballot(lane < limit && pre >= (double)p * ZK);
+        if (hit)
+          th = okey_inv((uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)hit) - 1));
+        else
+          good = 0;
+      }
+      if (lane == 0) {
+        S.pick = (int)__float_as_uint(th);
+        S.wn = good;
+      }
     }
     __syncthreads();
-    const uint64_t key = t < nw ? s_sorted[t] : 0ull;
+    thr = uni(__uint_as_float((uint32_t)S.pick));
+    ok = uni(S.wn) != 0;
+  } else if (ok) {
+    // rank by counting (keys are unique), scatter into descending order
+    if (t < nw) {
+      const uint64_t mine = S.wkey[t];
+      int rank = 0;
+      for (int q = 0; q < nw; ++q) rank += S.wkey[q] > mine ? 1 : 0;
+      S.sorted[rank] = mine;
+    }
+    __syncthreads();
+    const uint64_t key = t < nw ? S.sorted[t] : 0ull;
     const uint32_t kx = (uint32_t)(key >> 32);
-    const float x = okey_inv(kx);
-    const float e = t < nw ? ex2c((x - gm) * c) : 0.0f;
+    const float e = t < nw ? ex2c((okey_inv(kx) - gm) * c) : 0.0f;
     double pre, tot;
-    wg_scan<NW>((double)e, red, &pre, &tot);  // pre = inclusive prefix in sorted order
+    wg_scan<NW>((double)e, S.red, &pre, &tot);  // pre = inclusive prefix in sorted order
     double ZK = Z;
     int limit = nw;
     if (kon) {
       // k-th largest value (nw >= k unless the window hit the y >= -64 cutoff,
-      // in which case every element of the top-k set with non-negligible mass
-      // is in the window)
+      // in which case every top-k element with non-negligible mass is in it)
       uint32_t kk;
       if (k <= nw) {
-        if (t == k - 1) s_pick = (int)kx;
+        if (t == k - 1) S.pick = (int)kx;
         __syncthreads();
-        kk = uni((uint32_t)s_pick);
+        kk = uni((uint32_t)S.pick);
       } else {
-        kk = uni((uint32_t)(s_sorted[nw - 1] >> 32));
+        kk = uni((uint32_t)(S.sorted[nw - 1] >> 32));
       }
       const int inK = (t < nw && kx >= kk) ? 1 : 0;
-      limit = wg_sum_i<NW>(inK, red);
+      limit = wg_sum_i<NW>(inK, S.red);
       thr = uni(okey_inv(kk));
-      ZK = wg_sum<NW>((t == limit - 1) ? pre : 0.0, red);  // inclusive prefix at limit-1
+      ZK = wg_sum<NW>((t == limit - 1) ? pre : 0.0, S.red);  // inclusive prefix at limit-1
     }
     if (pon) {
-      const double target = (double)p * ZK;
-      const int first = (t < limit && pre >= target) ? t : 0x7fffffff;
-      const int q = wg_min_i<NW>(first, red);
+      const int first = (t < limit && pre >= (double)p * ZK) ? t : 0x7fffffff;
+      const int q = wg_min_i<NW>(first, S.red);
       if (q == 0x7fffffff) {
         ok = false;  // the window does not reach the top-p mass: exact path
       } else {
-        if (t == q) s_pick = (int)kx;
+        if (t == q) S.pick = (int)kx;
         __syncthreads();
-        thr = uni(okey_inv((uint32_t)s_pick));
+        thr = uni(okey_inv((uint32_t)S.pick));
       }
     }
     __syncthreads();
   }
 
   if (ok) {
-    cdf_pick<NT, CAP, T>(R, gm, c, true, thr, false, 0.0, u, s_cs, s_col, &P.out[b]);
+    double tmass = 0.0;
+    R.each([&](int, const uint4& v, float cmj) {
+      if (cmj >= thr) tmass += (double)esum_chunk_ge<T>(v, gm, c, thr);
+    });
+    cdf_pick<NT, T>(R, gm, c, true, thr, tmass, A.u, S, out);
   } else {
-    // Exact path on a global-memory view of the row (the register copy is
-    // dead from here on, which keeps this path off the hot path's registers).
-    MemRow<T, NT, VEC> M;
-    M.init(P.logits, r, P.ld, P.V);
-    thr = select_exact<NW, T>(M, gm, c, Z, kon, k, pon, p, red);
-    cdf_pick<NT, CAP, T>(M, gm, c, true, thr, false, 0.0, u, s_cs, s_col, &P.out[b]);
+    rare_row<T, NT, VEC>(P.logits, r, P.ld, P.V, 1, tm, gm, c, Z, k, p, A.u, &S, out);
+  }
+}
+
+// Output row b -> source row r: >= 0 valid, -1 past the end, -2 invalid gather index.
+__device__ __forceinline__ int64_t source_row(const SampleParams& P, int64_t b, int64_t nrows) {
+  if (b >= nrows) return -1;
+  const int64_t r = P.row_idx ? (int64_t)P.row_idx[b] : b;
+  return (r < 0 || r >= P.B_src) ? -2 : r;
+}
+
+template <bool GREEDY, typename T, int NT, int CAP, bool VEC>
+__device__ __forceinline__ void handle_row(RegRow<T, NT, CAP, VEC>& R, const SampleParams& P,
+                                           int64_t r, const RowArgs& A, int64_t b, Smem<NT>& S) {
+  if (r == -2) {
+    if (threadIdx.x == 0) P.out[b] = -1;
+    return;
+  }
+  if (GREEDY) greedy_row(R, &P.out[b], S);
+  else sample_row(R, P, r, A, &P.out[b], S);
+}
+
+// Issue the direct-to-LDS loads of a row: wave w's j-th load writes the 1 KiB
+// of chunks (w*L + j)*64 + lane to s_row at the same chunk position.  Lanes
+// whose chunk is partial or past the row end load a harmless in-row address;
+// RegRow::fetch_staged replaces those chunks.
+template <typename T, int NT, int CAP>
+__device__ __forceinline__ void stage_row(const char* base, uint32_t V, int L, uint4* s_row) {
+  constexpr int EPV = Elem<T>::EPV;
+  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    if (j < L) {
+      const uint32_t c = (w * (uint32_t)L + (uint32_t)j) * kWave + lane;
+      const bool full = c * EPV + EPV <= V;
+      const char* src = base + (full ? (uint32_t)(c * 16u) : 0u);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)src,
+          (__attribute__((address_space(3))) void*)(s_row + (w * (uint32_t)L + (uint32_t)j) * kWave), 16, 0,
+          0);
+    }
+  }
+}
+
+// Rows b = blockIdx.x, blockIdx.x + gridDim.x, ...
+//   STAGED: persistent; the next row streams into LDS (direct-to-LDS loads)
+//           while this row is processed from registers.
+//   else:   one row per workgroup.
+template <bool GREEDY, bool STAGED, typename T, int NT, int CAP, bool VEC>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void sampler_kernel(SampleParams P) {
+  __shared__ Smem<NT> S;
+  int64_t nrows = P.B_out;
+  if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
+  int64_t b = blockIdx.x;
+  if constexpr (!STAGED) {
+    const int64_t r = source_row(P, b, nrows);
+    if (r == -1) return;
+    RegRow<T, NT, CAP, VEC> R;
+    RowArgs A{};
+    if (r >= 0) {
+      A = row_args(P, r);
+      R.init(P.logits, r, P.ld, P.V);
+      R.fetch();
+    }
+    handle_row<GREEDY>(R, P, r, A, b, S);
+  } else {
+    __shared__ uint4 s_row[NT * CAP];
+    const int64_t G = gridDim.x;
+    int64_t r = source_row(P, b, nrows);
+    RegRow<T, NT, CAP, VEC> R;
+    if (r >= 0) {
+      R.init(P.logits, r, P.ld, P.V);
+      stage_row<T, NT, CAP>(R.base, R.V, R.L, s_row);
+    }
+    while (r != -1) {
+      // per-row arguments first: their loads then never queue behind the
+      // staging loads of the next row
+      RowArgs A{};
+      if (r >= 0) A = row_args(P, r);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // the staged row is complete and visible
+      if (r >= 0) {
+        R.init(P.logits, r, P.ld, P.V);
+        R.fetch_staged(s_row);
+      }
+      __syncthreads();  // every wave has read s_row
+      const int64_t bn = b + G;
+      const int64_t rn = source_row(P, bn, nrows);
+      if (rn >= 0) {
+        RowBase<T, NT, VEC> N;
+        N.init(P.logits, rn, P.ld, P.V);
+        stage_row<T, NT, CAP>(N.base, N.V, N.L, s_row);
+      }
+      handle_row<GREEDY>(R, P, r, A, b, S);
+      b = bn;
+      r = rn;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // Host launch.
 // ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP>
-static void launch_t(const SampleParams& P, int64_t B_out, bool greedy, bool vec,
-                     hipStream_t st) {
-  const dim3 grid((unsigned)B_out), block(NT);
-  if (greedy) {
-    if (vec) hipLaunchKernelGGL((greedy_kernel<T, NT, CAP, true>), grid, block, 0, st, P);
-    else hipLaunchKernelGGL((greedy_kernel<T, NT, CAP, false>), grid, block, 0, st, P);
-  } else {
-    if (vec) hipLaunchKernelGGL((sample_kernel<T, NT, CAP, true>), grid, block, 0, st, P);
-    else hipLaunchKernelGGL((sample_kernel<T, NT, CAP, false>), grid, block, 0, st, P);
+static int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
   }
+  return cached[dev];
+}
+
+template <bool GREEDY, bool STAGED, typename T, int NT, int CAP, bool VEC>
+static void launch_k(const SampleParams& P, hipStream_t st) {
+  int64_t grid = P.B_out;
+  if (STAGED) {
+    // persistent: as many workgroups as fit at once (LDS and registers allow
+    // one 1024-thread or four 256-thread workgroups per CU)
+    const int per_cu = NT >= 1024 ? 1 : 4;
+    grid = std::min<int64_t>(P.B_out, (int64_t)num_cus() * per_cu);
+  }
+  hipLaunchKernelGGL((sampler_kernel<GREEDY, STAGED, T, NT, CAP, VEC>), dim3((unsigned)grid), dim3(NT), 0,
+                     st, P);
 }
 
 template <typename T>
-static int launch_dtype(const SampleParams& P, int64_t B_out, bool greedy, bool vec,
-                        hipStream_t st) {
+static int launch_dtype(const SampleParams& P, bool greedy, bool vec, hipStream_t st) {
   constexpr int EPV = Elem<T>::EPV;
   const int64_t NV = (P.V + EPV - 1) / EPV;
-  // Workgroup size: the row fits in registers when NV <= NT * CAP.
-  if (NV <= 256 * 8) launch_t<T, 256, 8>(P, B_out, greedy, vec, st);
-  else if (NV <= 512 * 16) launch_t<T, 512, 16>(P, B_out, greedy, vec, st);
-  else if (NV <= (int64_t)1024 * kLMax) launch_t<T, 1024, 16>(P, B_out, greedy, vec, st);
-  else return set_error(LSG_ERR_ARG, "lsg_sample: V=%lld too large (max %lld elements)",
-                        (long long)P.V, (long long)1024 * kLMax * EPV);
+  // The row lives in registers when NV <= NT * CAP.  Aligned rows of up to
+  // 8192 chunks (128 KiB) use the persistent kernel with LDS staging; longer
+  // rows stream the chunks past NT * CAP.  Chunk byte offsets are 32-bit.
+  if (NV >= (int64_t)1 << 27)
+    return set_error(LSG_ERR_ARG, "lsg_sample: V=%lld too large", (long long)P.V);
+  auto go = [&](auto greedy_tag) {
+    constexpr bool G = decltype(greedy_tag)::value;
+    if (!vec) launch_k<G, false, T, 1024, 16, false>(P, st);
+    else if (NV <= 256 * 8) launch_k<G, true, T, 256, 8, true>(P, st);
+    else if (NV <= 1024 * 8) launch_k<G, true, T, 1024, 8, true>(P, st);
+    else launch_k<G, false, T, 1024, 16, true>(P, st);
+  };
+  if (greedy) go(std::true_type{});
+  else go(std::false_type{});
   return LSG_OK;
 }
 
@@ -679,14 +894,14 @@ extern "C" int lsg_sample(const void* logits, int dtype, int64_t B_src, int64_t 
   if (B_out == 0) return LSG_OK;
   const size_t es = dtype == kF32 ? 4 : 2;
   const bool vec = ((uintptr_t)logits % 16 == 0) && ((ld * (int64_t)es) % 16 == 0);
-  SampleParams P{logits, B_src, V, ld, temperatures, top_k, top_p, uniforms,
+  SampleParams P{logits, B_src, V, ld, B_out, temperatures, top_k, top_p, uniforms,
                  row_idx, n_rows_dev, out_ids};
   const bool greedy = temperatures == nullptr;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int rc;
-  if (dtype == kF32) rc = launch_dtype<float>(P, B_out, greedy, vec, st);
-  else if (dtype == kBF16) rc = launch_dtype<bf16_t>(P, B_out, greedy, vec, st);
-  else rc = launch_dtype<f16_t>(P, B_out, greedy, vec, st);
+  if (dtype == kF32) rc = launch_dtype<float>(P, greedy, vec, st);
+  else if (dtype == kBF16) rc = launch_dtype<bf16_t>(P, greedy, vec, st);
+  else rc = launch_dtype<f16_t>(P, greedy, vec, st);
   if (rc != LSG_OK) return rc;
   return check_launch("lsg_sample");
 }

@@ -102,7 +102,8 @@ def test_gate_cdb_four_steps(lsg, orc, dev):
         zc = z.cpu().numpy()
         assert np.array_equal(zc[(amb & 4) == 0], ref["z"][(amb & 4) == 0])
         Fg = res.state.cpu().numpy()
-        np.testing.assert_allclose(Fg, ref["F_next"], atol=1e-5)
+        zok = (amb & 4) == 0  # z cannot round differently under fp32 accumulation
+        np.testing.assert_allclose(Fg[zok], ref["F_next"][zok], atol=1e-5)
         # given the same z, F' is bit-exact
         same = zc == ref["z"]
         assert np.array_equal(Fg[same], ref["F_next"][same])
@@ -135,7 +136,8 @@ def test_gate_shapes_and_options(lsg, orc, dev, dtype, B, H):
             clean = (ref["amb"] & 1) == 0
             mask = res.signal.cpu().numpy().astype(np.uint8)
             assert np.array_equal(mask[clean], ref["mask"][clean])
-            np.testing.assert_allclose(res.state.cpu().numpy(), ref["F_next"], atol=1e-5)
+            zok = (ref["amb"] & 4) == 0
+            np.testing.assert_allclose(res.state.cpu().numpy()[zok], ref["F_next"][zok], atol=1e-5)
             _check_compaction(res, B)
 
 

