@@ -6,15 +6,14 @@
 //   torch.argmax (greedy)     sample.py:110-111 (+ int32 cast, model_runner.py:279-280)
 //   sample_impl -> flashinfer softmax / *_sampling_from_probs   sample.py:60-81
 //
-// One workgroup samples one row at a time.  The row is read from HBM exactly
-// once with coalesced 128-bit loads (wave w owns a contiguous span of the row
-// and reads it 1 KiB per instruction) and stays in VGPRs (CAP chunks of 16 B
-// per thread); the later passes (softmax normaliser, threshold search, CDF
-// walk) run on registers and LDS.  For rows that fit twice in the register
-// budget the kernel is persistent and double-buffered: while a workgroup works
-// on one row, the loads of its next row are already in flight, so HBM streams
-// continuously.  Chunks past NT*CAP (very large V), and the rare exact slow
-// path of the threshold search, re-read the row from global memory.
+// One workgroup samples one row.  The row is read from HBM once with coalesced
+// 128-bit loads (each wave instruction reads 1 KiB of contiguous logits) and
+// held in registers for the two full passes (row maximum, softmax normaliser).
+// The later steps (top-k / top-p threshold, inverse-CDF walk) touch only the
+// few chunks whose maximum can matter and re-read those.  Rows of up to 65536
+// bf16/f16 (32768 fp32) elements use 1024-thread workgroups of at most 64
+// VGPRs, two resident per CU: one streams its row from HBM while the other
+// computes.
 //
 // Semantics (per row r, x = float32(logit), NaN treated as -inf):
 //   T <= 0 or non-finite, or max x non-finite  -> id = argmax (torch rules)
@@ -23,8 +22,8 @@
 //   P = {x in K : x >= tau}, tau = largest x with mass(x >= tau) >= p * mass(K)
 //   id = first index j in P (ascending) with cumsum_P(e)[j] > u * sum_P(e)
 // Sums above the 16-byte chunk level are accumulated in float64 in a fixed
-// order, so the result is deterministic and agrees with a float64 evaluation
-// to ~1e-7 relative.
+// order, so the result is deterministic and agrees with a float64 evaluation to
+// ~1e-7 relative.
 #include "lsg_capi_internal.h"
 #include "lsg_common.h"
 
@@ -34,7 +33,7 @@
 namespace lsg {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kBins = 64;   // thread-maximum histogram: bins of width 1 in log2 units
+constexpr int kBins = 64;  // histogram of y = log2(e / e_max): bins of width 1
 
 struct SampleParams {
   const void* logits;
@@ -48,18 +47,45 @@ struct SampleParams {
   int32_t* out;
 };
 
-// exp of the scaled, max-shifted logit.  The clamp folds into v_exp_f32 and
-// maps NaN (from a NaN logit) to 0.
+// exp2 clamped to [0, 1]; the clamp folds into v_exp_f32 and maps NaN (from a
+// NaN logit) to 0.
 __device__ __forceinline__ float ex2c(float y) {
   return __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(y), 0.0f, 1.0f);
 }
 
-template <typename T>
-__device__ __forceinline__ float esum_chunk(const uint4& v, float gm, float c) {
-  constexpr int EPV = Elem<T>::EPV;
-  float e[EPV];
-#pragma unroll
-  for (int i = 0; i < EPV; ++i) e[i] = ex2c((Elem<T>::get(v, i) - gm) * c);
+// Smallest float >= a*b.
+__device__ __forceinline__ float mul_up(float a, float b) {
+  const float p = __fmul_rn(a, b);
+  const float r = __builtin_fmaf(a, b, -p);  // a*b - p exactly (finite p)
+  if (!(r > 0.0f)) return p;
+  const uint32_t u = __float_as_uint(p);
+  if (p > 0.0f) return __uint_as_float(u + 1u);
+  if (p < 0.0f) return __uint_as_float(u - 1u);
+  return __uint_as_float(1u);
+}
+
+// Exponent map of one row: e(x) = 2^y(x), y(x) = (x - m) * c with c = log2(e)/T.
+// When |m*c| < 2^22, y is one fma against b = m*c rounded up: every exponent is
+// then <= 0 and all of them carry the same offset m*c - b in [-1/2, 0], which
+// cancels in every ratio.  Otherwise y = (x - m) * c.
+struct Ex {
+  float c, nb, gm;
+  bool fma;
+  __device__ __forceinline__ void init(float gm_, float c_) {
+    gm = gm_;
+    c = c_;
+    const float b = mul_up(gm, c);
+    fma = __builtin_fabsf(b) < 4194304.0f;
+    nb = -b;
+  }
+  __device__ __forceinline__ float y(float x) const {
+    return fma ? __builtin_fmaf(x, c, nb) : (x - gm) * c;
+  }
+  __device__ __forceinline__ float e(float x) const { return ex2c(y(x)); }
+};
+
+template <int EPV>
+__device__ __forceinline__ float tree_sum(float (&e)[EPV]) {
 #pragma unroll
   for (int w = 1; w < EPV; w <<= 1)
 #pragma unroll
@@ -67,21 +93,34 @@ __device__ __forceinline__ float esum_chunk(const uint4& v, float gm, float c) {
   return e[0];
 }
 
-// Same, counting only elements with x >= thr.
-template <typename T>
-__device__ __forceinline__ float esum_chunk_ge(const uint4& v, float gm, float c, float thr) {
+// Mass of one chunk (pairwise tree in fp32); FMA selects the exponent form.
+template <typename T, bool FMA>
+__device__ __forceinline__ float esum_chunk(const uint4& v, const Ex& X) {
   constexpr int EPV = Elem<T>::EPV;
   float e[EPV];
 #pragma unroll
   for (int i = 0; i < EPV; ++i) {
     const float x = Elem<T>::get(v, i);
-    e[i] = x >= thr ? ex2c((x - gm) * c) : 0.0f;
+    e[i] = ex2c(FMA ? __builtin_fmaf(x, X.c, X.nb) : (x - X.gm) * X.c);
   }
+  return tree_sum<EPV>(e);
+}
+template <typename T>
+__device__ __forceinline__ float esum_chunk(const uint4& v, const Ex& X) {
+  return X.fma ? esum_chunk<T, true>(v, X) : esum_chunk<T, false>(v, X);
+}
+
+// Same, counting only elements with x >= thr.
+template <typename T>
+__device__ __forceinline__ float esum_chunk_ge(const uint4& v, const Ex& X, float thr) {
+  constexpr int EPV = Elem<T>::EPV;
+  float e[EPV];
 #pragma unroll
-  for (int w = 1; w < EPV; w <<= 1)
-#pragma unroll
-    for (int i = 0; i < EPV; i += 2 * w) e[i] += e[i + w];
-  return e[0];
+  for (int i = 0; i < EPV; ++i) {
+    const float x = Elem<T>::get(v, i);
+    e[i] = x >= thr ? X.e(x) : 0.0f;
+  }
+  return tree_sum<EPV>(e);
 }
 
 template <typename T>
@@ -92,32 +131,19 @@ __device__ __forceinline__ int count_chunk_ge(const uint4& v, float thr) {
   return n;
 }
 
-// ---------------------------------------------------------------------------
-// Row access.  Wave-blocked layout: wave w owns chunks [w*L*64, (w+1)*L*64);
-// its j-th load reads the 64 consecutive chunks (w*L + j)*64 + lane (1 KiB).
-// Index order is therefore (wave, j, lane, element).
-// ---------------------------------------------------------------------------
-template <typename T, int NT, bool VEC>
-struct RowBase {
-  static constexpr int EPV = Elem<T>::EPV;
-  const char* base;
-  uint32_t V;
-  int L;
-  uint32_t c0;  // chunk index of this thread's j = 0 load
-  __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, int64_t Vv) {
-    base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)Elem<T>::kSize;
-    V = (uint32_t)uni((uint32_t)Vv);
-    const uint32_t NV = (V + EPV - 1) / EPV;
-    L = (int)((NV + NT - 1) / NT);
-    c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)L * kWave + (threadIdx.x & 63);
-  }
-  __device__ __forceinline__ uint32_t chunk_index(int j) const { return c0 + (uint32_t)j * kWave; }
-  __device__ __forceinline__ uint4 load(int j) const {
-    return load_chunk32<T, VEC>(base, chunk_index(j), V);
-  }
-  __device__ __forceinline__ uint32_t elem_index(int j, int i) const {
-    return chunk_index(j) * EPV + (uint32_t)i;
-  }
+// Significant low bit of the order-preserving key of a T value (its float
+// image has that many trailing zero bits, or ones for negative values).
+template <typename T>
+struct KeyShift {
+  static constexpr int value = 0;
+};
+template <>
+struct KeyShift<bf16_t> {
+  static constexpr int value = 16;
+};
+template <>
+struct KeyShift<f16_t> {
+  static constexpr int value = 13;
 };
 
 // Chunk maxima in registers.  For 16-bit inputs the maximum is an exact input
@@ -133,10 +159,16 @@ struct ChunkMax {
   }
   __device__ __forceinline__ void set(int j, float m) {
     uint32_t bits;
-    if constexpr (sizeof(T) == 2 && Elem<T>::EPV == 8 && std::is_same<T, bf16_t>::value)
+    if constexpr (std::is_same<T, bf16_t>::value) {
       bits = __float_as_uint(m) >> 16;
-    else
+    } else {
+      // The compiler evaluates the f16 maximum with v_max3_f16 and assumes it
+      // clears the upper half of the destination register; on gfx950 the VOP3
+      // form keeps it.  Make the value opaque so the mask below is kept.
       bits = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)m);
+      asm volatile("" : "+v"(bits));
+      bits &= 0xffffu;
+    }
     if (j & 1) w[j >> 1] = (w[j >> 1] & 0x0000ffffu) | (bits << 16);
     else w[j >> 1] = (w[j >> 1] & 0xffff0000u) | bits;
   }
@@ -156,82 +188,14 @@ struct ChunkMax<float, CAP> {
   }
 };
 
-// Row copy in registers for j < CAP (+ chunk maxima); j >= CAP streams.
-template <typename T, int NT, int CAP, bool VEC>
-struct RegRow : RowBase<T, NT, VEC> {
-  using B = RowBase<T, NT, VEC>;
-  uint4 d[CAP];
-  ChunkMax<T, CAP> cm;
-  __device__ __forceinline__ void fetch() {
-#pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (j < B::L) d[j] = B::load(j);
-  }
-  // Registers from a row staged in LDS (chunk c at s_row[c]); partial and
-  // padding chunks, which the staging loads skipped, come from global memory.
-  __device__ __forceinline__ void fetch_staged(const uint4* s_row) {
-    constexpr int EPV = Elem<T>::EPV;
-#pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (j < B::L) {
-        const uint32_t c = B::chunk_index(j);
-        d[j] = (c * EPV + EPV <= B::V) ? s_row[c] : B::load(j);
-      }
-  }
-  // Tell the compiler the register copy may have changed, so values derived
-  // from it (unpacked floats) are recomputed per pass instead of being hoisted
-  // and kept live across passes (which would double the register footprint).
-  __device__ __forceinline__ void launder() {
-#pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      asm volatile("" : "+v"(d[j].x), "+v"(d[j].y), "+v"(d[j].z), "+v"(d[j].w));
-    cm.launder();
-  }
-  // Apply f(j, chunk, chunk_max) to every chunk this thread owns, in index order.
-  template <class F>
-  __device__ __forceinline__ void each(F&& f) {
-    launder();
-#pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (j < B::L) f(j, d[j], cm.get(j));
-    for (int j = CAP; j < B::L; ++j) {
-      const uint4 v = B::load(j);
-      f(j, v, chunk_max<T>(v));
-    }
-  }
-  // Chunk with a runtime (workgroup-uniform) index, built with masked ORs: a
-  // select chain would be folded back into a dynamic index, which moves d[] to
-  // scratch memory.
-  __device__ __forceinline__ uint4 chunk(int j) const {
-    if (j >= CAP) return B::load(j);
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-    for (int jj = 0; jj < CAP; ++jj) {
-      const uint32_t m = 0u - (uint32_t)(jj == j);
-      v.x |= d[jj].x & m;
-      v.y |= d[jj].y & m;
-      v.z |= d[jj].z & m;
-      v.w |= d[jj].w & m;
-    }
-    return v;
-  }
-};
+// Tell the compiler a register chunk may have changed, so values derived from it
+// (unpacked floats) are recomputed per pass instead of being hoisted and kept
+// live across passes (which would double the register footprint).
+__device__ __forceinline__ void launder(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
 
-// Row re-read from global memory on every pass (exact slow path).
-template <typename T, int NT, bool VEC>
-struct MemRow : RowBase<T, NT, VEC> {
-  using B = RowBase<T, NT, VEC>;
-  template <class F>
-  __device__ __forceinline__ void each(F&& f) {
-    for (int j = 0; j < B::L; ++j) {
-      const uint4 v = B::load(j);
-      f(j, v, chunk_max<T>(v));
-    }
-  }
-  __device__ __forceinline__ uint4 chunk(int j) const { return B::load(j); }
-};
-
-// LDS shared by the per-row routines (one row at a time per workgroup).
+// LDS shared by the per-row routines.
 template <int NT>
 struct Smem {
   static constexpr int NW = NT / kWave;
@@ -246,20 +210,125 @@ struct Smem {
   int pick;
 };
 
-// argmax with torch semantics.  gm is the NaN-ignoring maximum, tm this
-// thread's.  Returns the id (identical in every thread).
-template <int NW, typename T, class Row>
-__device__ __forceinline__ int32_t row_argmax(Row& R, float tm, float gm, double* red) {
+// ---------------------------------------------------------------------------
+// A row in registers.  Wave-blocked layout: wave w owns chunks
+// [w*L*64, (w+1)*L*64); its j-th load reads the 64 consecutive chunks
+// (w*L + j)*64 + lane (1 KiB of contiguous HBM), so the index order is (wave,
+// j, lane, element).  Chunks j < CAP stay in registers for the two full passes
+// (row maximum, softmax normaliser); their maxima stay for the rest of the row.
+// Later passes touch only the chunks whose maximum can matter and re-read them
+// (they are still in L2 or the Infinity Cache).  Chunks j >= CAP (very long
+// rows) are re-read on every pass.  FULL: the row is exactly NT*CAP full
+// chunks (every thread holds CAP chunks, no partial or padding chunk), so
+// loads and loops need no bounds checks.
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int CAP, bool VEC, bool FULL>
+struct Row {
+  static constexpr int EPV = Elem<T>::EPV;
+  const char* base;
+  uint32_t V;
+  int L;
+  uint32_t c0;  // chunk index of this thread's j = 0 load
+  uint4 d[CAP];
+  ChunkMax<T, CAP> cm;
+
+  __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, int64_t Vv) {
+    base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)Elem<T>::kSize;
+    V = (uint32_t)uni((uint32_t)Vv);
+    const uint32_t NV = (V + EPV - 1) / EPV;
+    L = FULL ? CAP : (int)((NV + NT - 1) / NT);
+    c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)L * kWave + (threadIdx.x & 63);
+  }
+  // chunk j is one of this thread's chunks
+  __device__ __forceinline__ bool has(int j) const { return FULL ? j < CAP : j < L; }
+  __device__ __forceinline__ int nstream() const { return FULL ? CAP : L; }  // loops j in [CAP, nstream())
+  __device__ __forceinline__ uint32_t chunk_index(int j) const { return c0 + (uint32_t)j * kWave; }
+  __device__ __forceinline__ uint4 load(int j) const {
+    if (FULL) return *reinterpret_cast<const uint4*>(base + chunk_index(j) * 16u);
+    return load_chunk32<T, VEC>(base, chunk_index(j), V);
+  }
+  __device__ __forceinline__ uint32_t elem_index(int j, int i) const {
+    return chunk_index(j) * EPV + (uint32_t)i;
+  }
+  __device__ __forceinline__ void fetch() {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) d[j] = has(j) ? load(j) : Elem<T>::pad();
+  }
+  // Pass A: chunk maxima (NANPROP: NaN-propagating, else NaN ignored); returns
+  // this thread's maximum.
+  template <bool NANPROP>
+  __device__ __forceinline__ float maxima() {
+    float tm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (has(j)) {
+        const float m = NANPROP ? chunk_maximum<T>(d[j]) : chunk_max<T>(d[j]);
+        cm.set(j, m);
+        tm = NANPROP ? fmaximum(tm, m) : fmaxf(tm, m);
+      }
+    for (int j = CAP; j < nstream(); ++j) {
+      const uint4 v = load(j);
+      tm = NANPROP ? fmaximum(tm, chunk_maximum<T>(v)) : fmaxf(tm, chunk_max<T>(v));
+    }
+    return tm;
+  }
+  // f(j, chunk, chunk_max) over every chunk, from registers where held.
+  template <bool NANPROP, class F>
+  __device__ __forceinline__ void each_reg(F&& f) {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      uint4 v = d[j];
+      launder(v);
+      if (has(j)) f(j, v, cm.get(j));
+    }
+    for (int j = CAP; j < nstream(); ++j) {
+      const uint4 v = load(j);
+      f(j, v, NANPROP ? chunk_maximum<T>(v) : chunk_max<T>(v));
+    }
+  }
+  // f(j, chunk_max) over every chunk (NaN-ignoring maxima).
+  template <class F>
+  __device__ __forceinline__ void each_cm(F&& f) {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (has(j)) f(j, cm.get(j));
+    for (int j = CAP; j < nstream(); ++j) f(j, chunk_max<T>(load(j)));
+  }
+  // f(j, chunk, chunk_max) over the chunks whose maximum passes keep(), re-read
+  // from memory.
+  template <class K, class F>
+  __device__ __forceinline__ void each_kept(K&& keep, F&& f) {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (has(j)) {
+        const float m = cm.get(j);
+        if (keep(m)) f(j, load(j), m);
+      }
+    for (int j = CAP; j < nstream(); ++j) {
+      const uint4 v = load(j);
+      const float m = chunk_max<T>(v);
+      if (keep(m)) f(j, v, m);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// argmax with torch semantics over a row whose chunk maxima ignore NaN.  gm is
+// the NaN-ignoring maximum, tm this thread's.  Returns the id (identical in
+// every thread).
+// ---------------------------------------------------------------------------
+template <int NW, typename T, class R_>
+__device__ __forceinline__ int32_t row_argmax(R_& R, float tm, float gm, double* red) {
   constexpr int EPV = Elem<T>::EPV;
   int nan = 0;
-  R.each([&](int, const uint4& v, float) {
+  R.template each_reg<false>([&](int, const uint4& v, float) {
 #pragma unroll
     for (int i = 0; i < EPV; ++i) nan |= __builtin_isnan(Elem<T>::get(v, i)) ? 1 : 0;
   });
   const int gnan = wg_max_i<NW>(nan, red);
   int first = 0x7fffffff;
   if (gnan ? nan : (tm == gm)) {
-    R.each([&](int j, const uint4& v, float) {
+    R.template each_reg<false>([&](int j, const uint4& v, float) {
 #pragma unroll
       for (int i = 0; i < EPV; ++i) {
         const float x = Elem<T>::get(v, i);
@@ -272,154 +341,54 @@ __device__ __forceinline__ int32_t row_argmax(Row& R, float tm, float gm, double
   return wg_min_i<NW>(first, red);
 }
 
-// ---------------------------------------------------------------------------
-// Exact threshold search by bisection over order-preserving float keys.
-// Returns thr: keep-mask x >= thr (top-k, then top-p within it).
-// ---------------------------------------------------------------------------
-template <int NW, typename T, class Row>
-__device__ float select_exact(Row& R, float gm, float c, double Z, bool kon, int32_t k, bool pon,
-                              float p, double* red) {
+// Exact threshold search by bisection over order-preserving keys (16 steps for
+// bf16, 19 for f16, 32 for fp32).  Returns thr: keep-mask x >= thr (top-k,
+// then top-p within it).  Chunks whose maximum is below the probe are skipped.
+template <int NW, typename T, class R_>
+__device__ __forceinline__ float select_exact(R_& R, const Ex& X, double Z, bool kon, int32_t k, bool pon,
+                                              float p, double* red) {
+  constexpr int SH = KeyShift<T>::value;
+  const uint32_t kmin = okey(-INFINITY) >> SH;
+  auto th_of = [&](uint32_t kk) { return kk <= kmin ? -INFINITY : okey_inv(kk << SH); };
+  const uint32_t khi = (okey(X.gm) >> SH) + 1u;
   float floor_thr = -INFINITY;
   if (kon) {
-    uint32_t lo = okey(-INFINITY), hi = okey(gm) + 1u;
+    uint32_t lo = kmin, hi = khi;
     while (hi - lo > 1u) {
       const uint32_t mid = lo + ((hi - lo) >> 1);
-      const float th = okey_inv(mid);
+      const float th = th_of(mid);
       int n = 0;
-      R.each([&](int, const uint4& v, float cmj) {
-        if (cmj >= th) n += count_chunk_ge<T>(v, th);
-      });
+      R.each_kept([&](float m) { return m >= th; },
+                  [&](int, const uint4& v, float) { n += count_chunk_ge<T>(v, th); });
       if (wg_sum_i<NW>(n, red) >= k) lo = mid;
       else hi = mid;
     }
-    floor_thr = okey_inv(lo);
+    floor_thr = th_of(lo);
   }
   if (!pon) return floor_thr;
   double zk = Z;
   if (kon) {
     double acc = 0.0;
-    R.each([&](int, const uint4& v, float cmj) {
-      if (cmj >= floor_thr) acc += (double)esum_chunk_ge<T>(v, gm, c, floor_thr);
-    });
+    R.each_kept([&](float m) { return m >= floor_thr; },
+                [&](int, const uint4& v, float) { acc += (double)esum_chunk_ge<T>(v, X, floor_thr); });
     zk = wg_sum<NW>(acc, red);
   }
   const double target = (double)p * zk;
-  uint32_t lo = okey(floor_thr), hi = okey(gm) + 1u;
+  uint32_t lo = floor_thr == -INFINITY ? kmin : (okey(floor_thr) >> SH), hi = khi;
   while (hi - lo > 1u) {
     const uint32_t mid = lo + ((hi - lo) >> 1);
-    const float th = okey_inv(mid);
+    const float th = th_of(mid);
     double ms = 0.0;
-    R.each([&](int, const uint4& v, float cmj) {
-      if (cmj >= th) ms += (double)esum_chunk_ge<T>(v, gm, c, th);
-    });
+    R.each_kept([&](float m) { return m >= th; },
+                [&](int, const uint4& v, float) { ms += (double)esum_chunk_ge<T>(v, X, th); });
     if (wg_sum<NW>(ms, red) >= target) lo = mid;
     else hi = mid;
   }
-  return okey_inv(lo);
+  return th_of(lo);
 }
 
-// ---------------------------------------------------------------------------
-// Inverse CDF in ascending index order over {x >= thr} (all when !masked).
-// Index order is (wave, j, lane, element): find the wave whose prefix crosses
-// U = u * total, then (inside that wave only) the column j, then the lane,
-// then the element.  The wave that holds the crossing recomputes its chunk
-// masses with the same arithmetic that produced the totals, so every level
-// sees identical values and the walk is deterministic.  tmass is this
-// thread's mass (all its chunks, masked like the walk).
-// ---------------------------------------------------------------------------
-template <int NT, typename T, class Row>
-__device__ __forceinline__ void cdf_pick(Row& R, float gm, float c, bool masked, float thr,
-                                         double tmass, float u, Smem<NT>& S, int32_t* out) {
-  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
-  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  {
-    const double ws = wave_sum(tmass);
-    if (lane == 0) S.col[wid] = ws;
-  }
-  __syncthreads();
-  // Wave totals in index order: lane w of every wave holds wave w's total and a
-  // wave scan gives the prefixes (identical in every wave).
-  int wstar;
-  double base, U;
-  {
-    const double sw = lane < NW ? S.col[lane] : 0.0;
-    const double inc = wave_incl_scan(sw, lane);
-    const double total = readlane_d(inc, NW - 1);
-    U = (double)u * total;
-    const uint64_t cross = __ballot(lane < NW && inc > U);
-    if (cross) {
-      wstar = __ffsll((unsigned long long)cross) - 1;
-    } else {  // u >= 1 or rounding: the last wave with mass
-      const uint64_t pos = __ballot(lane < NW && sw > 0.0);
-      wstar = pos ? 63 - __clzll((long long)pos) : 0;
-    }
-    wstar = uni(wstar);
-    base = readlane_d(wave_shr1(inc), wstar);
-  }
-  if (wid != wstar) return;
-  // column j inside the wave: one pass over this wave's chunks in index order
-  int jstar = -1, jlast = 0;
-  double jbase = base, cum = base, cum_last = base;
-  float sme = 0.0f, slast = 0.0f;
-  R.each([&](int j, const uint4& v, float cmj) {
-    const float sj = masked ? (cmj >= thr ? esum_chunk_ge<T>(v, gm, c, thr) : 0.0f)
-                            : esum_chunk<T>(v, gm, c);
-    const double col = wave_sum((double)sj);
-    if (col > 0.0) {
-      jlast = j;
-      slast = sj;
-      cum_last = cum;
-    }
-    if (jstar < 0 && cum + col > U) {
-      jstar = j;
-      jbase = cum;
-      sme = sj;
-    }
-    cum += col;
-  });
-  if (jstar < 0) {  // u >= 1 or rounding: the last column with mass
-    jstar = jlast;
-    jbase = cum_last;
-    sme = slast;
-  }
-  jstar = uni(jstar);
-  // lane inside the column
-  const double incl = wave_incl_scan((double)sme, lane);
-  const double excl = wave_shr1(incl);
-  const uint64_t bal = __ballot((sme > 0.0f) && (jbase + incl > U));
-  int owner;
-  if (bal) {
-    owner = __ffsll((unsigned long long)bal) - 1;
-  } else {
-    const uint64_t pos = __ballot(sme > 0.0f);
-    owner = pos ? 63 - __clzll((long long)pos) : 0;
-  }
-  const uint4 vj = R.chunk(jstar);
-  if (lane == owner) {
-    double acc = jbase + excl;
-    int pick = -1, lastpos = -1;
-#pragma unroll
-    for (int i = 0; i < EPV; ++i) {
-      const float x = Elem<T>::get(vj, i);
-      const float e = (!masked || x >= thr) ? ex2c((x - gm) * c) : 0.0f;
-      if (e > 0.0f) {
-        lastpos = i;
-        acc += (double)e;
-        if (pick < 0 && acc > U) pick = i;
-      }
-    }
-    if (pick < 0) pick = lastpos < 0 ? 0 : lastpos;
-    *out = (int32_t)R.elem_index(jstar, pick);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Candidate window bounded by a histogram of distinct elements (the thread
-// maxima, or the chunk maxima): since they are distinct elements, the window
-// {y >= lo} holds >= k elements once >= k of them have y >= lo, and holds mass
-// >= p*Z once those with y >= lo carry that much mass.  Returns the bin b (the
-// window is y >= -(b+1)) or -1 when no bin reaches the target.
-// ---------------------------------------------------------------------------
+// Histogram scan: the first bin b (from the top) at which the cumulative count
+// reaches k (top-k) or the cumulative mass reaches p*Z (top-p); -1 if none.
 template <int NT>
 __device__ __forceinline__ int window_bin(Smem<NT>& S, bool kon, int32_t k, float p, double Z) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -439,191 +408,16 @@ __device__ __forceinline__ int window_bin(Smem<NT>& S, bool kon, int32_t k, floa
 
 __device__ __forceinline__ int ybin(float y) { return min(kBins - 1, (int)(-y)); }
 
-// ---------------------------------------------------------------------------
-// One sampling row: row r of the logits -> out[b].  Every path is uniform
-// across the workgroup (all threads reach the same barriers).
-// ---------------------------------------------------------------------------
-struct RowArgs {
-  float T, p, u;
-  int32_t k;
-};
-
-__device__ __forceinline__ RowArgs row_args(const SampleParams& P, int64_t r) {
-  RowArgs a;
-  a.T = P.temps ? uni(P.temps[r]) : 0.0f;
-  a.u = P.uniforms ? uni(P.uniforms[r]) : 0.0f;
-  a.k = uni(P.top_k ? P.top_k[r] : 0);
-  a.p = uni(P.top_p ? P.top_p[r] : 1.0f);
-  return a;
-}
-
-// ---------------------------------------------------------------------------
-// Rare rows, outside the hot path's register allocation: they re-read the row
-// from global memory.
-//   mode 0: argmax (T <= 0, or a non-finite maximum, inside a sampling batch)
-//   mode 1: exact top-k / top-p threshold, then the masked CDF walk
-// ---------------------------------------------------------------------------
-template <typename T, int NT, bool VEC>
-__device__ __attribute__((noinline)) void rare_row(const void* logits, int64_t r, int64_t ld,
-                                                   int64_t V, int mode, float tm, float gm, float c,
-                                                   double Z, int32_t k, float p, float u,
-                                                   Smem<NT>* Sp, int32_t* out) {
+// Threshold from a collected window of nw <= kWin candidates (S.wkey: order key
+// of the value in the high word, ~index in the low word).  Returns false when
+// the window does not reach the top-p mass (the exact search then decides).
+template <int NT>
+__device__ bool window_threshold(Smem<NT>& S, int nw, bool kon, int32_t k, bool pon, float p, double Z,
+                                 const Ex& X, float* thr_out) {
   constexpr int NW = NT / kWave;
-  Smem<NT>& S = *Sp;
-  MemRow<T, NT, VEC> M;
-  M.init(logits, r, ld, V);
-  if (mode == 0) {
-    const int32_t id = row_argmax<NW, T>(M, tm, gm, S.red);
-    if (threadIdx.x == 0) *out = id;
-    return;
-  }
-  const bool kon = k >= 1 && (int64_t)k < V, pon = p < 1.0f;
-  const float thr = select_exact<NW, T>(M, gm, c, Z, kon, k, pon, p, S.red);
-  double tmass = 0.0;
-  M.each([&](int, const uint4& v, float cmj) {
-    if (cmj >= thr) tmass += (double)esum_chunk_ge<T>(v, gm, c, thr);
-  });
-  cdf_pick<NT, T>(M, gm, c, true, thr, tmass, u, S, out);
-}
-
-// ---------------------------------------------------------------------------
-// Greedy row: torch.argmax.  NaN-propagating maxima make a NaN anywhere the
-// row maximum, so one pass finds both the maximum and whether NaN is present;
-// the chunk maxima then point at the single chunk holding the first hit.
-// ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC>
-__device__ __forceinline__ void greedy_row(RegRow<T, NT, CAP, VEC>& R, int32_t* out, Smem<NT>& S) {
-  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
-  __syncthreads();
-  float tm = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < CAP; ++j)
-    if (j < R.L) {
-      const float m = chunk_maximum<T>(R.d[j]);
-      R.cm.set(j, m);
-      tm = fmaximum(tm, m);
-    }
-  for (int j = CAP; j < R.L; ++j) tm = fmaximum(tm, chunk_maximum<T>(R.load(j)));
-  const float gm = wg_maximum<NW>(tm, S.red);
-  const bool isn = gm != gm;
-  int first = 0x7fffffff;
-  if (isn ? (tm != tm) : (tm == gm)) {
-    R.each([&](int j, const uint4& v, float cmj) {
-      if (first == 0x7fffffff && (j >= CAP || (isn ? cmj != cmj : cmj == gm))) {
-#pragma unroll
-        for (int i = 0; i < EPV; ++i) {
-          const float x = Elem<T>::get(v, i);
-          const uint32_t idx = R.elem_index(j, i);
-          if (first == 0x7fffffff && (isn ? x != x : x == gm) && idx < R.V) first = (int)idx;
-        }
-      }
-    });
-  }
-  const int32_t id = wg_min_i<NW>(first, S.red);
-  if (threadIdx.x == 0) *out = id;
-}
-
-// ---------------------------------------------------------------------------
-// One sampling row: row r of the logits -> *out.  Every path is uniform across
-// the workgroup (all threads reach the same barriers).
-// ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC>
-__device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const SampleParams& P,
-                                           int64_t r, const RowArgs& A, int32_t* out, Smem<NT>& S) {
-  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
-  constexpr int kWin = Smem<NT>::kWin;
   const int t = threadIdx.x, wid = t >> 6;
-  __syncthreads();  // the previous row's readers of S are done
-
-  // ---- pass A: chunk maxima and the row maximum (NaN ignored) ------------
-  float tm = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < CAP; ++j)
-    if (j < R.L) {
-      const float m = chunk_max<T>(R.d[j]);
-      R.cm.set(j, m);
-      tm = fmaxf(tm, m);
-    }
-  for (int j = CAP; j < R.L; ++j) tm = fmaxf(tm, chunk_max<T>(R.load(j)));
-  const float gm = wg_max<NW>(tm, S.red);
-
-  if (!(A.T > 0.0f) || !(A.T < INFINITY) || !(gm > -INFINITY) || !(gm < INFINITY)) {
-    rare_row<T, NT, VEC>(P.logits, r, P.ld, P.V, 0, tm, gm, 0.0f, 0.0, 0, 1.0f, 0.0f, &S, out);
-    return;
-  }
-  const float c = kLog2e / A.T;
-
-  // ---- pass B: softmax normaliser ------------------------------------------
-  R.launder();
-  double zt = 0.0;
-#pragma unroll
-  for (int j = 0; j < CAP; ++j)
-    if (j < R.L) zt += (double)esum_chunk<T>(R.d[j], gm, c);
-  for (int j = CAP; j < R.L; ++j) zt += (double)esum_chunk<T>(R.load(j), gm, c);
-  const double Z = wg_sum<NW>(zt, S.red);
-
-  const int32_t k = A.k;
-  const float p = A.p;
-  const bool kon = k >= 1 && (int64_t)k < (int64_t)R.V;
-  const bool pon = p < 1.0f;
-  if (!kon && !pon) {
-    cdf_pick<NT, T>(R, gm, c, false, -INFINITY, zt, A.u, S, out);
-    return;
-  }
-
-  // ---- candidate window from the thread maxima, else the chunk maxima (two
-  // heavy tokens can share a thread, rarely a 16-byte chunk) ----------------
-  if (t < kBins) {
-    S.hcnt[t] = 0;
-    S.hmass[t] = 0.0f;
-  }
-  if (t == 0) S.wn = 0;
-  __syncthreads();
-  {
-    const float ytm = (tm - gm) * c;
-    if (ytm >= -64.0f) {
-      atomicAdd(&S.hcnt[ybin(ytm)], 1);
-      atomicAdd(&S.hmass[ybin(ytm)], ex2c(ytm));
-    }
-  }
-  int bin = window_bin(S, kon, k, p, Z);
-  if (bin < 0) {
-    if (t < kBins) {
-      S.hcnt[t] = 0;
-      S.hmass[t] = 0.0f;
-    }
-    __syncthreads();
-    R.each([&](int, const uint4&, float cmj) {
-      const float y = (cmj - gm) * c;
-      if (y >= -64.0f) {
-        atomicAdd(&S.hcnt[ybin(y)], 1);
-        atomicAdd(&S.hmass[ybin(y)], ex2c(y));
-      }
-    });
-    bin = window_bin(S, kon, k, p, Z);
-  }
-  const float lo_y = -(float)((bin < 0 ? kBins - 1 : bin) + 1);
-
-  // collect the window (chunk maxima prune almost every chunk)
-  R.each([&](int j, const uint4& v, float cmj) {
-    if ((cmj - gm) * c >= lo_y) {
-#pragma unroll
-      for (int i = 0; i < EPV; ++i) {
-        const float x = Elem<T>::get(v, i);
-        if ((x - gm) * c >= lo_y) {
-          const int pos = atomicAdd(&S.wn, 1);
-          if (pos < kWin) {
-            const uint32_t idx = R.elem_index(j, i);
-            S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - idx);
-          }
-        }
-      }
-    }
-  });
-  __syncthreads();
-  const int nw = uni(S.wn);
-  bool ok = nw <= kWin;
   float thr = -INFINITY;
+  bool ok = true;
   if (nw <= kWave) {
     // Small window: wave 0 ranks, scans and thresholds it alone.
     if (wid == 0) {
@@ -631,15 +425,16 @@ __device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const Sam
       const uint64_t mine = lane < nw ? S.wkey[lane] : 0ull;
       int rank = 0;
       for (int q = 0; q < nw; ++q) {
-        const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
-                               (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
+        const uint64_t other =
+            ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
+            (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
         rank += other > mine ? 1 : 0;
       }
       if (lane < nw) S.sorted[rank] = mine;
       __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
       const uint64_t key = lane < nw ? S.sorted[lane] : 0ull;
       const uint32_t kx = (uint32_t)(key >> 32);
-      const float e = lane < nw ? ex2c((okey_inv(kx) - gm) * c) : 0.0f;
+      const float e = lane < nw ? X.e(okey_inv(kx)) : 0.0f;
       const double pre = wave_incl_scan((double)e, lane);  // inclusive prefix in sorted order
       double ZK = Z;
       int limit = nw;
@@ -654,7 +449,8 @@ __device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const Sam
       if (pon) {
         const uint64_t hit = __ballot(lane < limit && pre >= (double)p * ZK);
         if (hit)
-          th = okey_inv((uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)hit) - 1));
+          th = okey_inv(
+              (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)hit) - 1));
         else
           good = 0;
       }
@@ -666,7 +462,7 @@ __device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const Sam
     __syncthreads();
     thr = uni(__uint_as_float((uint32_t)S.pick));
     ok = uni(S.wn) != 0;
-  } else if (ok) {
+  } else {
     // rank by counting (keys are unique), scatter into descending order
     if (t < nw) {
       const uint64_t mine = S.wkey[t];
@@ -677,14 +473,13 @@ __device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const Sam
     __syncthreads();
     const uint64_t key = t < nw ? S.sorted[t] : 0ull;
     const uint32_t kx = (uint32_t)(key >> 32);
-    const float e = t < nw ? ex2c((okey_inv(kx) - gm) * c) : 0.0f;
+    const float e = t < nw ? X.e(okey_inv(kx)) : 0.0f;
     double pre, tot;
     wg_scan<NW>((double)e, S.red, &pre, &tot);  // pre = inclusive prefix in sorted order
     double ZK = Z;
     int limit = nw;
     if (kon) {
-      // k-th largest value (nw >= k unless the window hit the y >= -64 cutoff,
-      // in which case every top-k element with non-negligible mass is in it)
+      // k-th largest value (the window holds at least k elements)
       uint32_t kk;
       if (k <= nw) {
         if (t == k - 1) S.pick = (int)kx;
@@ -702,7 +497,7 @@ __device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const Sam
       const int first = (t < limit && pre >= (double)p * ZK) ? t : 0x7fffffff;
       const int q = wg_min_i<NW>(first, S.red);
       if (q == 0x7fffffff) {
-        ok = false;  // the window does not reach the top-p mass: exact path
+        ok = false;
       } else {
         if (t == q) S.pick = (int)kx;
         __syncthreads();
@@ -711,16 +506,181 @@ __device__ __forceinline__ void sample_row(RegRow<T, NT, CAP, VEC>& R, const Sam
     }
     __syncthreads();
   }
+  *thr_out = thr;
+  return ok;
+}
 
-  if (ok) {
-    double tmass = 0.0;
-    R.each([&](int, const uint4& v, float cmj) {
-      if (cmj >= thr) tmass += (double)esum_chunk_ge<T>(v, gm, c, thr);
-    });
-    cdf_pick<NT, T>(R, gm, c, true, thr, tmass, A.u, S, out);
-  } else {
-    rare_row<T, NT, VEC>(P.logits, r, P.ld, P.V, 1, tm, gm, c, Z, k, p, A.u, &S, out);
+// Top-k / top-p threshold from a candidate window.  The window {y >= lo} is
+// bounded with a histogram of distinct elements (the thread maxima, else the
+// chunk maxima): once >= k of them have y >= lo, the window holds >= k
+// elements, and once those carry mass >= p*Z, it holds the top-p set.  Returns
+// false when no small window exists (the exact search then decides).
+template <int NT, typename T, class R_>
+__device__ __forceinline__ bool find_threshold(R_& R, float tm, const Ex& X, double Z, bool kon, int32_t k,
+                                               bool pon, float p, Smem<NT>& S, float* thr) {
+  constexpr int EPV = Elem<T>::EPV, kWin = Smem<NT>::kWin;
+  const int t = threadIdx.x;
+  if (t < kBins) {
+    S.hcnt[t] = 0;
+    S.hmass[t] = 0.0f;
   }
+  if (t == 0) S.wn = 0;
+  __syncthreads();
+  {
+    const float y = X.y(tm);
+    if (y >= -64.0f) {
+      atomicAdd(&S.hcnt[ybin(y)], 1);
+      atomicAdd(&S.hmass[ybin(y)], ex2c(y));
+    }
+  }
+  int bin = window_bin(S, kon, k, p, Z);
+  if (bin < 0) {
+    if (t < kBins) {
+      S.hcnt[t] = 0;
+      S.hmass[t] = 0.0f;
+    }
+    __syncthreads();
+    R.each_cm([&](int, float cmj) {
+      const float y = X.y(cmj);
+      if (y >= -64.0f) {
+        atomicAdd(&S.hcnt[ybin(y)], 1);
+        atomicAdd(&S.hmass[ybin(y)], ex2c(y));
+      }
+    });
+    bin = window_bin(S, kon, k, p, Z);
+    if (bin < 0) return false;
+  }
+  const float lo_y = -(float)(bin + 1);
+  R.each_kept([&](float m) { return X.y(m) >= lo_y; },
+              [&](int j, const uint4& v, float) {
+#pragma unroll
+                for (int i = 0; i < EPV; ++i) {
+                  const float x = Elem<T>::get(v, i);
+                  if (X.y(x) >= lo_y) {
+                    const int pos = atomicAdd(&S.wn, 1);
+                    if (pos < kWin)
+                      S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
+                  }
+                }
+              });
+  __syncthreads();
+  const int nw = uni(S.wn);
+  if (nw > kWin) return false;
+  return window_threshold<NT>(S, nw, kon, k, pon, p, Z, X, thr);
+}
+
+// ---------------------------------------------------------------------------
+// Inverse CDF in ascending index order over {x >= thr} (all when !masked).
+// Index order is (wave, j, lane, element): find the wave whose prefix crosses
+// U = u * total, then (inside that wave only) the column j, then the lane,
+// then the element.  csum[j*NT + t] holds thread t's mass of register chunk j
+// and tmass its total, both computed with the arithmetic the walk repeats, so
+// every level sees identical values and the walk is deterministic.
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int CAP, bool VEC, bool FULL>
+__device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, const float* csum, double tmass,
+                                         bool masked, float thr, const Ex& X, float u, Smem<NT>& S,
+                                         int32_t* out) {
+  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  {
+    const double ws = wave_sum(tmass);
+    if (lane == 0) S.col[wid] = ws;
+  }
+  __syncthreads();
+  int wstar;
+  double base, U;
+  {
+    const double sw = lane < NW ? S.col[lane] : 0.0;
+    const double inc = wave_incl_scan(sw, lane);
+    const double total = readlane_d(inc, NW - 1);
+    U = (double)u * total;
+    const uint64_t cross = __ballot(lane < NW && inc > U);
+    if (cross) {
+      wstar = __ffsll((unsigned long long)cross) - 1;
+    } else {  // u >= 1 or rounding: the last wave with mass
+      const uint64_t pos = __ballot(lane < NW && sw > 0.0);
+      wstar = pos ? 63 - __clzll((long long)pos) : 0;
+    }
+    wstar = uni(wstar);
+    base = readlane_d(wave_shr1(inc), wstar);
+  }
+  if (wid != wstar) return;
+  // column j inside the wave
+  int jstar = -1, jlast = 0;
+  double jbase = base, cum = base, cum_last = base;
+  float sme = 0.0f, slast = 0.0f;
+  auto column = [&](int j, float sj) {
+    const double col = wave_sum((double)sj);
+    if (col > 0.0) {
+      jlast = j;
+      slast = sj;
+      cum_last = cum;
+    }
+    if (jstar < 0 && cum + col > U) {
+      jstar = j;
+      jbase = cum;
+      sme = sj;
+    }
+    cum += col;
+  };
+#pragma unroll
+  for (int j = 0; j < CAP; ++j)
+    if (R.has(j)) column(j, csum[j * NT + threadIdx.x]);
+  for (int j = CAP; j < R.nstream(); ++j) {
+    const uint4 v = R.load(j);
+    column(j, masked ? (chunk_max<T>(v) >= thr ? esum_chunk_ge<T>(v, X, thr) : 0.0f) : esum_chunk<T>(v, X));
+  }
+  if (jstar < 0) {
+    jstar = jlast;
+    jbase = cum_last;
+    sme = slast;
+  }
+  jstar = uni(jstar);
+  // lane inside the column
+  const double incl = wave_incl_scan((double)sme, lane);
+  const double excl = wave_shr1(incl);
+  const uint64_t bal = __ballot((sme > 0.0f) && (jbase + incl > U));
+  int owner;
+  if (bal) {
+    owner = __ffsll((unsigned long long)bal) - 1;
+  } else {
+    const uint64_t pos = __ballot(sme > 0.0f);
+    owner = pos ? 63 - __clzll((long long)pos) : 0;
+  }
+  if (lane != owner) return;
+  const uint4 v = R.load(jstar);
+  double acc = jbase + excl;
+  int pick = -1, lastpos = -1;
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    const float x = Elem<T>::get(v, i);
+    const float e = (!masked || x >= thr) ? X.e(x) : 0.0f;
+    if (e > 0.0f) {
+      lastpos = i;
+      acc += (double)e;
+      if (pick < 0 && acc > U) pick = i;
+    }
+  }
+  if (pick < 0) pick = lastpos < 0 ? 0 : lastpos;
+  *out = (int32_t)R.elem_index(jstar, pick);
+}
+
+// ---------------------------------------------------------------------------
+// Per-row arguments (uniform loads through the scalar cache).
+// ---------------------------------------------------------------------------
+struct RowArgs {
+  float T, p, u;
+  int32_t k;
+};
+
+__device__ __forceinline__ RowArgs row_args(const SampleParams& P, int64_t r) {
+  RowArgs a;
+  a.T = P.temps ? uni(P.temps[r]) : 0.0f;
+  a.u = P.uniforms ? uni(P.uniforms[r]) : 0.0f;
+  a.k = uni(P.top_k ? P.top_k[r] : 0);
+  a.p = uni(P.top_p ? P.top_p[r] : 1.0f);
+  return a;
 }
 
 // Output row b -> source row r: >= 0 valid, -1 past the end, -2 invalid gather index.
@@ -730,143 +690,150 @@ __device__ __forceinline__ int64_t source_row(const SampleParams& P, int64_t b, 
   return (r < 0 || r >= P.B_src) ? -2 : r;
 }
 
-template <bool GREEDY, typename T, int NT, int CAP, bool VEC>
-__device__ __forceinline__ void handle_row(RegRow<T, NT, CAP, VEC>& R, const SampleParams& P,
-                                           int64_t r, const RowArgs& A, int64_t b, Smem<NT>& S) {
+// ---------------------------------------------------------------------------
+// Greedy row: torch.argmax.  NaN-propagating maxima make a NaN anywhere the
+// row maximum, so one pass finds both the maximum and whether NaN is present;
+// the chunk maxima then point at the chunk holding the first hit.
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int CAP, bool VEC, bool FULL>
+__device__ __forceinline__ void row_greedy(Row<T, NT, CAP, VEC, FULL>& R, int32_t* out, Smem<NT>& S) {
+  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
+  const float tm = R.template maxima<true>();
+  const float gm = wg_maximum<NW>(tm, S.red);
+  const bool isn = gm != gm;
+  int first = 0x7fffffff;
+  if (isn ? (tm != tm) : (tm == gm)) {
+    R.template each_reg<true>([&](int j, const uint4& v, float cmj) {
+      if (first == 0x7fffffff && (isn ? cmj != cmj : cmj == gm)) {
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+          const float x = Elem<T>::get(v, i);
+          const uint32_t idx = R.elem_index(j, i);
+          if (first == 0x7fffffff && (isn ? x != x : x == gm) && idx < R.V) first = (int)idx;
+        }
+      }
+    });
+  }
+  const int32_t id = wg_min_i<NW>(first, S.red);
+  if (threadIdx.x == 0) *out = id;
+}
+
+// Pass B: register chunk masses s[] and this thread's total.
+template <bool FMA, typename T, int NT, int CAP, bool VEC, bool FULL>
+__device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float* csum) {
+  double tmass = 0.0;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    uint4 v = R.d[j];
+    launder(v);
+    const float sj = R.has(j) ? esum_chunk<T, FMA>(v, X) : 0.0f;
+    csum[j * NT + threadIdx.x] = sj;
+    tmass += (double)sj;
+  }
+  for (int j = CAP; j < R.nstream(); ++j) tmass += (double)esum_chunk<T, FMA>(R.load(j), X);
+  return tmass;
+}
+
+// ---------------------------------------------------------------------------
+// One sampling row.  Every branch is uniform across the workgroup.
+// ---------------------------------------------------------------------------
+template <typename T, int NT, int CAP, bool VEC, bool FULL>
+__device__ __forceinline__ void row_sample(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
+                                           Smem<NT>& S, float* csum) {
+  constexpr int NW = NT / kWave;
+  const float tm = R.template maxima<false>();
+  const float gm = wg_max<NW>(tm, S.red);
+  if (!(A.T > 0.0f) || !(A.T < INFINITY) || !(gm > -INFINITY) || !(gm < INFINITY)) {
+    const int32_t id = row_argmax<NW, T>(R, tm, gm, S.red);
+    if (threadIdx.x == 0) *out = id;
+    return;
+  }
+  Ex X;
+  X.init(gm, kLog2e / A.T);
+  double tmass = X.fma ? row_masses<true>(R, X, csum) : row_masses<false>(R, X, csum);
+  const bool kon = A.k >= 1 && (uint32_t)A.k < R.V, pon = A.p < 1.0f;
+  if (!kon && !pon) {
+    cdf_walk(R, csum, tmass, false, -INFINITY, X, A.u, S, out);
+    return;
+  }
+  const double Z = wg_sum<NW>(tmass, S.red);
+  float thr;
+  if (!find_threshold<NT, T>(R, tm, X, Z, kon, A.k, pon, A.p, S, &thr))
+    thr = select_exact<NW, T>(R, X, Z, kon, A.k, pon, A.p, S.red);
+  tmass = 0.0;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    float sj = 0.0f;
+    if (R.has(j) && R.cm.get(j) >= thr) sj = esum_chunk_ge<T>(R.load(j), X, thr);
+    csum[j * NT + threadIdx.x] = sj;
+    tmass += (double)sj;
+  }
+  for (int j = CAP; j < R.nstream(); ++j) {
+    const uint4 v = R.load(j);
+    if (chunk_max<T>(v) >= thr) tmass += (double)esum_chunk_ge<T>(v, X, thr);
+  }
+  cdf_walk(R, csum, tmass, true, thr, X, A.u, S, out);
+}
+
+// One workgroup per output row b (grid = B_out).  WPE waves per SIMD: 8 lets two
+// 1024-thread workgroups share a CU, so one streams its row while the other
+// computes.
+template <bool GREEDY, typename T, int NT, int CAP, bool VEC, bool FULL, int WPE>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
+void sampler_kernel(SampleParams P) {
+  __shared__ Smem<NT> S;
+  __shared__ float csum[GREEDY ? 1 : NT * CAP];  // chunk masses, [j][thread]
+  int64_t nrows = P.B_out;
+  if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
+  const int64_t b = blockIdx.x;
+  const int64_t r = source_row(P, b, nrows);
+  if (r == -1) return;
   if (r == -2) {
     if (threadIdx.x == 0) P.out[b] = -1;
     return;
   }
-  if (GREEDY) greedy_row(R, &P.out[b], S);
-  else sample_row(R, P, r, A, &P.out[b], S);
+  RowArgs A{};
+  if (!GREEDY) A = row_args(P, r);
+  Row<T, NT, CAP, VEC, FULL> R;
+  R.init(P.logits, r, P.ld, P.V);
+  R.fetch();
+  if (GREEDY) row_greedy(R, &P.out[b], S);
+  else row_sample(R, A, &P.out[b], S, csum);
 }
 
-// Issue the direct-to-LDS loads of a row: wave w's j-th load writes the 1 KiB
-// of chunks (w*L + j)*64 + lane to s_row at the same chunk position.  Lanes
-// whose chunk is partial or past the row end load a harmless in-row address;
-// RegRow::fetch_staged replaces those chunks.
-template <typename T, int NT, int CAP>
-__device__ __forceinline__ void stage_row(const char* base, uint32_t V, int L, uint4* s_row) {
+// ---------------------------------------------------------------------------
+// Host launch.  One workgroup per output row; rows past the device row count
+// (n_rows_dev) exit at once.
+//   chunks per row NV <= 256*8    256 threads, 8 chunks each in registers
+//   NV <= 1024*8                  1024 threads, 8 chunks each (two per CU)
+//   longer rows                   1024 threads, 16 chunks each, the rest streamed
+// Unaligned rows (row start or stride not 16-byte aligned) use element loads.
+// ---------------------------------------------------------------------------
+template <class K>
+static void launch(K kernel, int NT, const SampleParams& P, hipStream_t st) {
+  hipLaunchKernelGGL(kernel, dim3((unsigned)P.B_out), dim3(NT), 0, st, P);
+}
+
+template <typename T, bool G>
+static void launch_rows(const SampleParams& P, bool vec, hipStream_t st) {
   constexpr int EPV = Elem<T>::EPV;
-  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-  for (int j = 0; j < CAP; ++j) {
-    if (j < L) {
-      const uint32_t c = (w * (uint32_t)L + (uint32_t)j) * kWave + lane;
-      const bool full = c * EPV + EPV <= V;
-      const char* src = base + (full ? (uint32_t)(c * 16u) : 0u);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)src,
-          (__attribute__((address_space(3))) void*)(s_row + (w * (uint32_t)L + (uint32_t)j) * kWave), 16, 0,
-          0);
-    }
-  }
-}
-
-// Rows b = blockIdx.x, blockIdx.x + gridDim.x, ...
-//   STAGED: persistent; the next row streams into LDS (direct-to-LDS loads)
-//           while this row is processed from registers.
-//   else:   one row per workgroup.
-template <bool GREEDY, bool STAGED, typename T, int NT, int CAP, bool VEC>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8)))
-void sampler_kernel(SampleParams P) {
-  __shared__ Smem<NT> S;
-  int64_t nrows = P.B_out;
-  if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
-  int64_t b = blockIdx.x;
-  if constexpr (!STAGED) {
-    const int64_t r = source_row(P, b, nrows);
-    if (r == -1) return;
-    RegRow<T, NT, CAP, VEC> R;
-    RowArgs A{};
-    if (r >= 0) {
-      A = row_args(P, r);
-      R.init(P.logits, r, P.ld, P.V);
-      R.fetch();
-    }
-    handle_row<GREEDY>(R, P, r, A, b, S);
-  } else {
-    __shared__ uint4 s_row[NT * CAP];
-    const int64_t G = gridDim.x;
-    int64_t r = source_row(P, b, nrows);
-    RegRow<T, NT, CAP, VEC> R;
-    if (r >= 0) {
-      R.init(P.logits, r, P.ld, P.V);
-      stage_row<T, NT, CAP>(R.base, R.V, R.L, s_row);
-    }
-    while (r != -1) {
-      // per-row arguments first: their loads then never queue behind the
-      // staging loads of the next row
-      RowArgs A{};
-      if (r >= 0) A = row_args(P, r);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();  // the staged row is complete and visible
-      if (r >= 0) {
-        R.init(P.logits, r, P.ld, P.V);
-        R.fetch_staged(s_row);
-      }
-      __syncthreads();  // every wave has read s_row
-      const int64_t bn = b + G;
-      const int64_t rn = source_row(P, bn, nrows);
-      if (rn >= 0) {
-        RowBase<T, NT, VEC> N;
-        N.init(P.logits, rn, P.ld, P.V);
-        stage_row<T, NT, CAP>(N.base, N.V, N.L, s_row);
-      }
-      handle_row<GREEDY>(R, P, r, A, b, S);
-      b = bn;
-      r = rn;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Host launch.
-// ---------------------------------------------------------------------------
-static int num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
-template <bool GREEDY, bool STAGED, typename T, int NT, int CAP, bool VEC>
-static void launch_k(const SampleParams& P, hipStream_t st) {
-  int64_t grid = P.B_out;
-  if (STAGED) {
-    // persistent: as many workgroups as fit at once (LDS and registers allow
-    // one 1024-thread or four 256-thread workgroups per CU)
-    const int per_cu = NT >= 1024 ? 1 : 4;
-    grid = std::min<int64_t>(P.B_out, (int64_t)num_cus() * per_cu);
-  }
-  hipLaunchKernelGGL((sampler_kernel<GREEDY, STAGED, T, NT, CAP, VEC>), dim3((unsigned)grid), dim3(NT), 0,
-                     st, P);
+  const int64_t NV = (P.V + EPV - 1) / EPV;
+  if (!vec) launch(sampler_kernel<G, T, 1024, 16, false, false, 4>, 1024, P, st);
+  else if (NV <= 256 * 8) launch(sampler_kernel<G, T, 256, 8, true, false, 8>, 256, P, st);
+  else if (NV == 1024 * 8 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 8, true, true, 8>, 1024, P, st);
+  else if (NV <= 1024 * 8) launch(sampler_kernel<G, T, 1024, 8, true, false, 8>, 1024, P, st);
+  else launch(sampler_kernel<G, T, 1024, 16, true, false, 4>, 1024, P, st);
 }
 
 template <typename T>
 static int launch_dtype(const SampleParams& P, bool greedy, bool vec, hipStream_t st) {
   constexpr int EPV = Elem<T>::EPV;
   const int64_t NV = (P.V + EPV - 1) / EPV;
-  // The row lives in registers when NV <= NT * CAP.  Aligned rows of up to
-  // 8192 chunks (128 KiB) use the persistent kernel with LDS staging; longer
-  // rows stream the chunks past NT * CAP.  Chunk byte offsets are 32-bit.
+  // Chunk byte offsets are 32-bit.
   if (NV >= (int64_t)1 << 27)
     return set_error(LSG_ERR_ARG, "lsg_sample: V=%lld too large", (long long)P.V);
-  auto go = [&](auto greedy_tag) {
-    constexpr bool G = decltype(greedy_tag)::value;
-    if (!vec) launch_k<G, false, T, 1024, 16, false>(P, st);
-    else if (NV <= 256 * 8) launch_k<G, true, T, 256, 8, true>(P, st);
-    else if (NV <= 1024 * 8) launch_k<G, true, T, 1024, 8, true>(P, st);
-    else launch_k<G, false, T, 1024, 16, true>(P, st);
-  };
-  if (greedy) go(std::true_type{});
-  else go(std::false_type{});
+  if (greedy) launch_rows<T, true>(P, vec, st);
+  else launch_rows<T, false>(P, vec, st);
   return LSG_OK;
 }
 
