@@ -33,7 +33,13 @@
 namespace lsg {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kBins = 64;  // histogram of y = log2(e / e_max): bins of width 1
+constexpr int kBins = 64;  // histogram of y = log2(e / e_max): bins of width 1/2
+constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
+// Margin on the top-p histogram test: the bin is chosen where the float sum of
+// the binned maxima reaches p*Z*(1 + 2^-10), so the window (a superset of those
+// maxima, summed in double) always reaches p*Z despite the rounding of the
+// float atomic additions (at most 2048 terms: error < 2048 * 2^-24 < 2^-10).
+constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
 
 struct SampleParams {
   const void* logits;
@@ -78,11 +84,31 @@ struct Ex {
     fma = __builtin_fabsf(b) < 4194304.0f;
     nb = -b;
   }
+  // Same for wave-uniform arguments; the fields are kept in scalar registers.
+  __device__ __forceinline__ void init_u(float gm_, float c_) {
+    gm = uni(gm_);
+    c = uni(c_);
+    const float b = uni(mul_up(gm, c));
+    fma = __builtin_fabsf(b) < 4194304.0f;
+    nb = -b;
+  }
   __device__ __forceinline__ float y(float x) const {
     return fma ? __builtin_fmaf(x, c, nb) : (x - gm) * c;
   }
   __device__ __forceinline__ float e(float x) const { return ex2c(y(x)); }
 };
+
+// 2^(shift(a) - shift(b)): converts masses relative to a's maximum into masses
+// relative to b's (a.gm <= b.gm, same c).  The shift of the fma form is the
+// float -nb, that of the other form gm * c.
+__device__ __forceinline__ float shift_ratio(const Ex& a, const Ex& b) {
+  float d;
+  if (a.fma && b.fma) d = b.nb - a.nb;
+  else if (a.fma) d = __builtin_fmaf(-b.gm, b.c, -a.nb);
+  else if (b.fma) d = __builtin_fmaf(a.gm, a.c, b.nb);
+  else d = (a.gm - b.gm) * a.c;
+  return ex2c(d);
+}
 
 template <int EPV>
 __device__ __forceinline__ float tree_sum(float (&e)[EPV]) {
@@ -176,6 +202,14 @@ struct ChunkMax {
 #pragma unroll
     for (int i = 0; i < N; ++i) asm volatile("" : "+v"(w[i]));
   }
+  __device__ __forceinline__ void store(uint32_t* p) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = w[i];
+  }
+  __device__ __forceinline__ void load(const uint32_t* p) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = p[i];
+  }
 };
 template <int CAP>
 struct ChunkMax<float, CAP> {
@@ -186,6 +220,14 @@ struct ChunkMax<float, CAP> {
 #pragma unroll
     for (int i = 0; i < CAP; ++i) asm volatile("" : "+v"(m[i]));
   }
+  __device__ __forceinline__ void store(uint32_t* p) const {
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) p[i] = __float_as_uint(m[i]);
+  }
+  __device__ __forceinline__ void load(const uint32_t* p) {
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) m[i] = __uint_as_float(p[i]);
+  }
 };
 
 // Tell the compiler a register chunk may have changed, so values derived from it
@@ -195,13 +237,31 @@ __device__ __forceinline__ void launder(uint4& v) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
+// Chunk j of CAP register chunks with a runtime index, built with masked ORs:
+// a select chain would be folded back into a dynamic index, which moves the
+// array to scratch memory.
+template <int CAP>
+__device__ __forceinline__ uint4 select_chunk(const uint4 (&d)[CAP], int j) {
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int jj = 0; jj < CAP; ++jj) {
+    const uint32_t m = 0u - (uint32_t)(jj == j);
+    v.x |= d[jj].x & m;
+    v.y |= d[jj].y & m;
+    v.z |= d[jj].z & m;
+    v.w |= d[jj].w & m;
+  }
+  return v;
+}
+
 // LDS shared by the per-row routines.
 template <int NT>
 struct Smem {
   static constexpr int NW = NT / kWave;
   static constexpr int kWin = NT < 512 ? NT : 512;  // candidate window capacity
   double red[NW];
-  double col[NW];
+  double wtot[NW];  // per-wave masses
+  float wmax[NW];   // per-wave maxima
   int hcnt[kBins];
   float hmass[kBins];
   uint64_t wkey[kWin];    // candidate window (unsorted)
@@ -212,36 +272,35 @@ struct Smem {
 
 // ---------------------------------------------------------------------------
 // A row in registers.  Wave-blocked layout: wave w owns chunks
-// [w*L*64, (w+1)*L*64); its j-th load reads the 64 consecutive chunks
-// (w*L + j)*64 + lane (1 KiB of contiguous HBM), so the index order is (wave,
-// j, lane, element).  Chunks j < CAP stay in registers for the two full passes
-// (row maximum, softmax normaliser); their maxima stay for the rest of the row.
-// Later passes touch only the chunks whose maximum can matter and re-read them
-// (they are still in L2 or the Infinity Cache).  Chunks j >= CAP (very long
-// rows) are re-read on every pass.  FULL: the row is exactly NT*CAP full
-// chunks (every thread holds CAP chunks, no partial or padding chunk), so
-// loads and loops need no bounds checks.
+// [w*L*64, (w+1)*L*64) (L = chunks per thread); its j-th load reads the 64
+// consecutive chunks (w*L + j)*64 + lane (1 KiB of contiguous HBM), so the
+// index order is (wave, j, lane, element).  Chunks j < CAP stay in registers;
+// their maxima go to LDS.  Chunks j >= CAP (very long rows) are re-read on
+// every pass.  FULL: the row is exactly NT*CAP full chunks (every thread holds
+// CAP chunks, no partial or padding chunk), so loads need no bounds checks.
 // ---------------------------------------------------------------------------
 template <typename T, int NT, int CAP, bool VEC, bool FULL>
 struct Row {
   static constexpr int EPV = Elem<T>::EPV;
+  using CM = ChunkMax<T, CAP>;
+  static constexpr int kCmWords = sizeof(CM) / 4;
   const char* base;
   uint32_t V;
   int L;
   uint32_t c0;  // chunk index of this thread's j = 0 load
   uint4 d[CAP];
-  ChunkMax<T, CAP> cm;
+  uint32_t* cmx;  // this thread's chunk maxima in LDS (kCmWords words)
 
-  __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, int64_t Vv) {
+  __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, int64_t Vv, uint32_t* cm_lds) {
+    cmx = cm_lds + threadIdx.x * kCmWords;
     base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)Elem<T>::kSize;
     V = (uint32_t)uni((uint32_t)Vv);
     const uint32_t NV = (V + EPV - 1) / EPV;
     L = FULL ? CAP : (int)((NV + NT - 1) / NT);
     c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)L * kWave + (threadIdx.x & 63);
   }
-  // chunk j is one of this thread's chunks
   __device__ __forceinline__ bool has(int j) const { return FULL ? j < CAP : j < L; }
-  __device__ __forceinline__ int nstream() const { return FULL ? CAP : L; }  // loops j in [CAP, nstream())
+  __device__ __forceinline__ int nstream() const { return FULL ? CAP : L; }  // chunks of this thread
   __device__ __forceinline__ uint32_t chunk_index(int j) const { return c0 + (uint32_t)j * kWave; }
   __device__ __forceinline__ uint4 load(int j) const {
     if (FULL) return *reinterpret_cast<const uint4*>(base + chunk_index(j) * 16u);
@@ -254,60 +313,76 @@ struct Row {
 #pragma unroll
     for (int j = 0; j < CAP; ++j) d[j] = has(j) ? load(j) : Elem<T>::pad();
   }
-  // Pass A: chunk maxima (NANPROP: NaN-propagating, else NaN ignored); returns
-  // this thread's maximum.
+  // Pass A: chunk maxima (NANPROP: NaN-propagating, else NaN ignored) to LDS;
+  // returns this thread's maximum.
   template <bool NANPROP>
   __device__ __forceinline__ float maxima() {
     float tm = -INFINITY;
+    CM cm;
 #pragma unroll
-    for (int j = 0; j < CAP; ++j)
+    for (int j = 0; j < CAP; ++j) {
+      cm.set(j, -INFINITY);
       if (has(j)) {
         const float m = NANPROP ? chunk_maximum<T>(d[j]) : chunk_max<T>(d[j]);
         cm.set(j, m);
         tm = NANPROP ? fmaximum(tm, m) : fmaxf(tm, m);
       }
+    }
+    cm.store(cmx);
     for (int j = CAP; j < nstream(); ++j) {
       const uint4 v = load(j);
       tm = NANPROP ? fmaximum(tm, chunk_maximum<T>(v)) : fmaxf(tm, chunk_max<T>(v));
     }
     return tm;
   }
-  // f(j, chunk, chunk_max) over every chunk, from registers where held.
-  template <bool NANPROP, class F>
-  __device__ __forceinline__ void each_reg(F&& f) {
-#pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      uint4 v = d[j];
-      launder(v);
-      if (has(j)) f(j, v, cm.get(j));
-    }
-    for (int j = CAP; j < nstream(); ++j) {
-      const uint4 v = load(j);
-      f(j, v, NANPROP ? chunk_maximum<T>(v) : chunk_max<T>(v));
+  // Maximum of register chunk j, from LDS.
+  __device__ __forceinline__ float cm_at(int j) const {
+    if constexpr (sizeof(T) == 2) {
+      uint4 v;
+      v.x = cmx[j >> 1] >> ((j & 1) * 16);
+      return Elem<T>::get(v, 0);
+    } else {
+      return __uint_as_float(cmx[j]);
     }
   }
-  // f(j, chunk_max) over every chunk (NaN-ignoring maxima).
+  // The passes below run once per row on few chunks: compact loops (small code
+  // keeps them in the instruction cache), chunks picked with a runtime index.
+  __device__ __forceinline__ uint4 chunk(int j) const { return j < CAP ? select_chunk<CAP>(d, j) : load(j); }
+  // f(j, chunk_max) over every chunk (register chunks: the stored maxima).
   template <class F>
   __device__ __forceinline__ void each_cm(F&& f) {
-#pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (has(j)) f(j, cm.get(j));
-    for (int j = CAP; j < nstream(); ++j) f(j, chunk_max<T>(load(j)));
+#pragma unroll 1
+    for (int j = 0; j < nstream(); ++j) f(j, j < CAP ? cm_at(j) : chunk_max<T>(load(j)));
   }
-  // f(j, chunk, chunk_max) over the chunks whose maximum passes keep(), re-read
-  // from memory.
+  // f(j, chunk, chunk_max) over the chunks whose maximum passes keep().
   template <class K, class F>
   __device__ __forceinline__ void each_kept(K&& keep, F&& f) {
-#pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (has(j)) {
-        const float m = cm.get(j);
-        if (keep(m)) f(j, load(j), m);
+#pragma unroll 1
+    for (int j = 0; j < nstream(); ++j) {
+      if (j < CAP) {
+        const float m = cm_at(j);
+        if (keep(m)) f(j, select_chunk<CAP>(d, j), m);
+      } else {
+        const uint4 v = load(j);
+        const float m = chunk_max<T>(v);
+        if (keep(m)) f(j, v, m);
       }
-    for (int j = CAP; j < nstream(); ++j) {
-      const uint4 v = load(j);
-      const float m = chunk_max<T>(v);
-      if (keep(m)) f(j, v, m);
+    }
+  }
+  // Same, re-reading the chunks from memory (rare paths: the registers are
+  // then free for the path's own state).
+  template <class K, class F>
+  __device__ __forceinline__ void each_kept_mem(K&& keep, F&& f) {
+#pragma unroll 1
+    for (int j = 0; j < nstream(); ++j) {
+      if (j < CAP) {
+        const float m = cm_at(j);
+        if (keep(m)) f(j, load(j), m);
+      } else {
+        const uint4 v = load(j);
+        const float m = chunk_max<T>(v);
+        if (keep(m)) f(j, v, m);
+      }
     }
   }
 };
@@ -321,14 +396,14 @@ template <int NW, typename T, class R_>
 __device__ __forceinline__ int32_t row_argmax(R_& R, float tm, float gm, double* red) {
   constexpr int EPV = Elem<T>::EPV;
   int nan = 0;
-  R.template each_reg<false>([&](int, const uint4& v, float) {
+  R.each_kept_mem([](float) { return true; }, [&](int, const uint4& v, float) {
 #pragma unroll
     for (int i = 0; i < EPV; ++i) nan |= __builtin_isnan(Elem<T>::get(v, i)) ? 1 : 0;
   });
   const int gnan = wg_max_i<NW>(nan, red);
   int first = 0x7fffffff;
   if (gnan ? nan : (tm == gm)) {
-    R.template each_reg<false>([&](int j, const uint4& v, float) {
+    R.each_kept_mem([](float) { return true; }, [&](int j, const uint4& v, float) {
 #pragma unroll
       for (int i = 0; i < EPV; ++i) {
         const float x = Elem<T>::get(v, i);
@@ -358,8 +433,8 @@ __device__ __forceinline__ float select_exact(R_& R, const Ex& X, double Z, bool
       const uint32_t mid = lo + ((hi - lo) >> 1);
       const float th = th_of(mid);
       int n = 0;
-      R.each_kept([&](float m) { return m >= th; },
-                  [&](int, const uint4& v, float) { n += count_chunk_ge<T>(v, th); });
+      R.each_kept_mem([&](float m) { return m >= th; },
+                      [&](int, const uint4& v, float) { n += count_chunk_ge<T>(v, th); });
       if (wg_sum_i<NW>(n, red) >= k) lo = mid;
       else hi = mid;
     }
@@ -369,8 +444,8 @@ __device__ __forceinline__ float select_exact(R_& R, const Ex& X, double Z, bool
   double zk = Z;
   if (kon) {
     double acc = 0.0;
-    R.each_kept([&](float m) { return m >= floor_thr; },
-                [&](int, const uint4& v, float) { acc += (double)esum_chunk_ge<T>(v, X, floor_thr); });
+    R.each_kept_mem([&](float m) { return m >= floor_thr; },
+                    [&](int, const uint4& v, float) { acc += (double)esum_chunk_ge<T>(v, X, floor_thr); });
     zk = wg_sum<NW>(acc, red);
   }
   const double target = (double)p * zk;
@@ -379,8 +454,8 @@ __device__ __forceinline__ float select_exact(R_& R, const Ex& X, double Z, bool
     const uint32_t mid = lo + ((hi - lo) >> 1);
     const float th = th_of(mid);
     double ms = 0.0;
-    R.each_kept([&](float m) { return m >= th; },
-                [&](int, const uint4& v, float) { ms += (double)esum_chunk_ge<T>(v, X, th); });
+    R.each_kept_mem([&](float m) { return m >= th; },
+                    [&](int, const uint4& v, float) { ms += (double)esum_chunk_ge<T>(v, X, th); });
     if (wg_sum<NW>(ms, red) >= target) lo = mid;
     else hi = mid;
   }
@@ -396,7 +471,7 @@ __device__ __forceinline__ int window_bin(Smem<NT>& S, bool kon, int32_t k, floa
   if (wid == 0) {
     const int pc = wave_incl_scan_i(S.hcnt[lane], lane);
     const double pm = wave_incl_scan((double)S.hmass[lane], lane);
-    const bool ok = kon ? (pc >= k) : (pm >= (double)p * Z);
+    const bool ok = kon ? (pc >= k) : (pm >= (double)p * Z * kBinMargin);
     const uint64_t bal = __ballot(ok);
     if (lane == 0) S.pick = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
   }
@@ -406,7 +481,9 @@ __device__ __forceinline__ int window_bin(Smem<NT>& S, bool kon, int32_t k, floa
   return bin;
 }
 
-__device__ __forceinline__ int ybin(float y) { return min(kBins - 1, (int)(-y)); }
+__device__ __forceinline__ int ybin(float y) { return min(kBins - 1, (int)(-2.0f * y)); }
+// Lower edge of bin b.
+__device__ __forceinline__ float bin_floor(int b) { return -0.5f * (float)(b + 1); }
 
 // Threshold from a collected window of nw <= kWin candidates (S.wkey: order key
 // of the value in the high word, ~index in the low word).  Returns false when
@@ -528,7 +605,7 @@ __device__ __forceinline__ bool find_threshold(R_& R, float tm, const Ex& X, dou
   __syncthreads();
   {
     const float y = X.y(tm);
-    if (y >= -64.0f) {
+    if (y >= kYMin) {
       atomicAdd(&S.hcnt[ybin(y)], 1);
       atomicAdd(&S.hmass[ybin(y)], ex2c(y));
     }
@@ -542,7 +619,7 @@ __device__ __forceinline__ bool find_threshold(R_& R, float tm, const Ex& X, dou
     __syncthreads();
     R.each_cm([&](int, float cmj) {
       const float y = X.y(cmj);
-      if (y >= -64.0f) {
+      if (y >= kYMin) {
         atomicAdd(&S.hcnt[ybin(y)], 1);
         atomicAdd(&S.hmass[ybin(y)], ex2c(y));
       }
@@ -550,7 +627,7 @@ __device__ __forceinline__ bool find_threshold(R_& R, float tm, const Ex& X, dou
     bin = window_bin(S, kon, k, p, Z);
     if (bin < 0) return false;
   }
-  const float lo_y = -(float)(bin + 1);
+  const float lo_y = bin_floor(bin);
   R.each_kept([&](float m) { return X.y(m) >= lo_y; },
               [&](int j, const uint4& v, float) {
 #pragma unroll
@@ -567,103 +644,6 @@ __device__ __forceinline__ bool find_threshold(R_& R, float tm, const Ex& X, dou
   const int nw = uni(S.wn);
   if (nw > kWin) return false;
   return window_threshold<NT>(S, nw, kon, k, pon, p, Z, X, thr);
-}
-
-// ---------------------------------------------------------------------------
-// Inverse CDF in ascending index order over {x >= thr} (all when !masked).
-// Index order is (wave, j, lane, element): find the wave whose prefix crosses
-// U = u * total, then (inside that wave only) the column j, then the lane,
-// then the element.  csum[j*NT + t] holds thread t's mass of register chunk j
-// and tmass its total, both computed with the arithmetic the walk repeats, so
-// every level sees identical values and the walk is deterministic.
-// ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC, bool FULL>
-__device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, const float* csum, double tmass,
-                                         bool masked, float thr, const Ex& X, float u, Smem<NT>& S,
-                                         int32_t* out) {
-  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  {
-    const double ws = wave_sum(tmass);
-    if (lane == 0) S.col[wid] = ws;
-  }
-  __syncthreads();
-  int wstar;
-  double base, U;
-  {
-    const double sw = lane < NW ? S.col[lane] : 0.0;
-    const double inc = wave_incl_scan(sw, lane);
-    const double total = readlane_d(inc, NW - 1);
-    U = (double)u * total;
-    const uint64_t cross = __ballot(lane < NW && inc > U);
-    if (cross) {
-      wstar = __ffsll((unsigned long long)cross) - 1;
-    } else {  // u >= 1 or rounding: the last wave with mass
-      const uint64_t pos = __ballot(lane < NW && sw > 0.0);
-      wstar = pos ? 63 - __clzll((long long)pos) : 0;
-    }
-    wstar = uni(wstar);
-    base = readlane_d(wave_shr1(inc), wstar);
-  }
-  if (wid != wstar) return;
-  // column j inside the wave
-  int jstar = -1, jlast = 0;
-  double jbase = base, cum = base, cum_last = base;
-  float sme = 0.0f, slast = 0.0f;
-  auto column = [&](int j, float sj) {
-    const double col = wave_sum((double)sj);
-    if (col > 0.0) {
-      jlast = j;
-      slast = sj;
-      cum_last = cum;
-    }
-    if (jstar < 0 && cum + col > U) {
-      jstar = j;
-      jbase = cum;
-      sme = sj;
-    }
-    cum += col;
-  };
-#pragma unroll
-  for (int j = 0; j < CAP; ++j)
-    if (R.has(j)) column(j, csum[j * NT + threadIdx.x]);
-  for (int j = CAP; j < R.nstream(); ++j) {
-    const uint4 v = R.load(j);
-    column(j, masked ? (chunk_max<T>(v) >= thr ? esum_chunk_ge<T>(v, X, thr) : 0.0f) : esum_chunk<T>(v, X));
-  }
-  if (jstar < 0) {
-    jstar = jlast;
-    jbase = cum_last;
-    sme = slast;
-  }
-  jstar = uni(jstar);
-  // lane inside the column
-  const double incl = wave_incl_scan((double)sme, lane);
-  const double excl = wave_shr1(incl);
-  const uint64_t bal = __ballot((sme > 0.0f) && (jbase + incl > U));
-  int owner;
-  if (bal) {
-    owner = __ffsll((unsigned long long)bal) - 1;
-  } else {
-    const uint64_t pos = __ballot(sme > 0.0f);
-    owner = pos ? 63 - __clzll((long long)pos) : 0;
-  }
-  if (lane != owner) return;
-  const uint4 v = R.load(jstar);
-  double acc = jbase + excl;
-  int pick = -1, lastpos = -1;
-#pragma unroll
-  for (int i = 0; i < EPV; ++i) {
-    const float x = Elem<T>::get(v, i);
-    const float e = (!masked || x >= thr) ? X.e(x) : 0.0f;
-    if (e > 0.0f) {
-      lastpos = i;
-      acc += (double)e;
-      if (pick < 0 && acc > U) pick = i;
-    }
-  }
-  if (pick < 0) pick = lastpos < 0 ? 0 : lastpos;
-  *out = (int32_t)R.elem_index(jstar, pick);
 }
 
 // ---------------------------------------------------------------------------
@@ -703,44 +683,183 @@ __device__ __forceinline__ void row_greedy(Row<T, NT, CAP, VEC, FULL>& R, int32_
   const bool isn = gm != gm;
   int first = 0x7fffffff;
   if (isn ? (tm != tm) : (tm == gm)) {
-    R.template each_reg<true>([&](int j, const uint4& v, float cmj) {
-      if (first == 0x7fffffff && (isn ? cmj != cmj : cmj == gm)) {
-#pragma unroll
+    // first chunk whose (NaN-propagating) maximum is the hit, then its first element
+#pragma unroll 1
+    for (int j = 0; j < R.nstream() && first == 0x7fffffff; ++j) {
+      const uint4 v = R.chunk(j);
+      const float cmj = j < CAP ? R.cm_at(j) : chunk_maximum<T>(v);
+      if (isn ? cmj != cmj : cmj == gm) {
+#pragma unroll 1
         for (int i = 0; i < EPV; ++i) {
           const float x = Elem<T>::get(v, i);
           const uint32_t idx = R.elem_index(j, i);
           if (first == 0x7fffffff && (isn ? x != x : x == gm) && idx < R.V) first = (int)idx;
         }
       }
-    });
+    }
   }
   const int32_t id = wg_min_i<NW>(first, S.red);
   if (threadIdx.x == 0) *out = id;
 }
 
-// Pass B: register chunk masses s[] and this thread's total.
+// ---------------------------------------------------------------------------
+// Inverse CDF inside the crossing wave of a wave-blocked row: the column j,
+// then the lane, then the element whose prefix crosses U.  base is the mass of
+// the waves before this one (row reference), fw converts this wave's masses
+// into the row's reference (wave-uniform).  cs[j * NT] is this thread's mass of
+// register chunk j; chunk_mass(j) recomputes that of a chunk j >= CAP and
+// elem_mass(x) that of one element, with the arithmetic that produced cs.  REG:
+// the chosen chunk is taken from registers, else re-read.  The owner lane
+// writes the id.
+// ---------------------------------------------------------------------------
+template <bool REG, typename T, int NT, int CAP, bool VEC, bool FULL, class CMass, class EMass>
+__device__ __forceinline__ void wave_walk(Row<T, NT, CAP, VEC, FULL>& R, const float* cs, double fw, double base,
+                                          double U, CMass&& chunk_mass, EMass&& elem_mass, int32_t* out) {
+  constexpr int EPV = Elem<T>::EPV;
+  const int lane = threadIdx.x & 63;
+  int jstar = -1, jlast = 0;
+  double jbase = base, cum = base, cum_last = base;
+  float sme = 0.0f, slast = 0.0f;
+  auto column = [&](int j, float sj) {
+    const double col = wave_sum((double)sj) * fw;
+    if (col > 0.0) {
+      jlast = j;
+      slast = sj;
+      cum_last = cum;
+    }
+    if (jstar < 0 && cum + col > U) {
+      jstar = j;
+      jbase = cum;
+      sme = sj;
+    }
+    cum += col;
+  };
+#pragma unroll
+  for (int j = 0; j < CAP; ++j)
+    if (R.has(j)) column(j, cs[j * NT]);
+  for (int j = CAP; j < R.nstream(); ++j) column(j, chunk_mass(j));
+  if (jstar < 0) {
+    jstar = jlast;
+    jbase = cum_last;
+    sme = slast;
+  }
+  jstar = uni(jstar);
+  const double incl = wave_incl_scan((double)sme, lane) * fw;
+  const double excl = wave_shr1(incl);
+  int owner;
+  {
+    const uint64_t bal = __ballot(sme > 0.0f && jbase + incl > U);
+    if (bal) {
+      owner = __ffsll((unsigned long long)bal) - 1;
+    } else {
+      const uint64_t pos = __ballot(sme > 0.0f);
+      owner = pos ? 63 - __clzll((long long)pos) : 0;
+    }
+  }
+  if (lane != owner) return;
+  const uint4 v = REG ? R.chunk(jstar) : R.load(jstar);
+  double a = jbase + excl;
+  int pick = -1, lastpos = -1;
+#pragma unroll 1
+  for (int i = 0; i < EPV; ++i) {
+    const double e = (double)elem_mass(Elem<T>::get(v, i)) * fw;
+    if (e > 0.0) {
+      lastpos = i;
+      a += e;
+      if (pick < 0 && a > U) pick = i;
+    }
+  }
+  if (pick < 0) pick = lastpos < 0 ? 0 : lastpos;
+  *out = (int32_t)R.elem_index(jstar, pick);
+}
+
+// The crossing wave of U = u * (sum of the wave masses sw, one per lane < NW):
+// sets wstar and base (mass of the waves before it); returns U.
+template <int NW>
+__device__ __forceinline__ double cross_wave(double sw, float u, int* wstar, double* base) {
+  const int lane = threadIdx.x & 63;
+  const double inc = wave_incl_scan(sw, lane);
+  const double total = readlane_d(inc, NW - 1);
+  asm volatile("" : "+s"(u));  // convert here: a hoisted double copy would be spilled
+  const double U = (double)u * total;
+  int w;
+  const uint64_t cross = __ballot(lane < NW && inc > U);
+  if (cross) {
+    w = __ffsll((unsigned long long)cross) - 1;
+  } else {  // u >= 1 or rounding: the last wave with mass
+    const uint64_t pos = __ballot(lane < NW && sw > 0.0);
+    w = pos ? 63 - __clzll((long long)pos) : 0;
+  }
+  w = uni(w);
+  *wstar = w;
+  *base = readlane_d(wave_shr1(inc), w);
+  return U;
+}
+
+// Full inverse-CDF walk with the masses in the row's reference: wave totals
+// through LDS (one barrier), crossing wave, then wave_walk.
+template <bool REG, typename T, int NT, int CAP, bool VEC, bool FULL, class CMass, class EMass>
+__device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, double tmass, const float* cs,
+                                         CMass&& chunk_mass, EMass&& elem_mass, float u, Smem<NT>& S,
+                                         int32_t* out) {
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const double ws = wave_sum(tmass);
+  if (lane == 0) S.wtot[wid] = ws;
+  __syncthreads();
+  int wstar;
+  double base;
+  const double U = cross_wave<NW>(lane < NW ? S.wtot[lane] : 0.0, u, &wstar, &base);
+  if (wid != wstar) return;
+  wave_walk<REG>(R, cs, 1.0, base, U, chunk_mass, elem_mass, out);
+}
+
+// This thread's chunk masses (register chunks) -> cs[j * NT] in LDS and its
+// total mass (chunks past CAP included).
 template <bool FMA, typename T, int NT, int CAP, bool VEC, bool FULL>
-__device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float* csum) {
+__device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float* cs) {
   double tmass = 0.0;
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
     uint4 v = R.d[j];
-    launder(v);
+    launder(v);  // no unpacked value is shared with the maxima pass
     const float sj = R.has(j) ? esum_chunk<T, FMA>(v, X) : 0.0f;
-    csum[j * NT + threadIdx.x] = sj;
+    cs[j * NT] = sj;
     tmass += (double)sj;
   }
   for (int j = CAP; j < R.nstream(); ++j) tmass += (double)esum_chunk<T, FMA>(R.load(j), X);
   return tmass;
 }
 
+// Masked chunk masses (x >= thr, relative to X) -> cs and the total; chunks are
+// re-read from memory.
+template <typename T, int NT, int CAP, bool VEC, bool FULL>
+__device__ __forceinline__ double masked_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float thr, float* cs) {
+  double tmass = 0.0;
+#pragma unroll 1
+  for (int j = 0; j < R.nstream(); ++j) {
+    float sj = 0.0f;
+    if (j < CAP) {
+      if (R.has(j) && R.cm_at(j) >= thr) sj = esum_chunk_ge<T>(R.load(j), X, thr);
+      cs[j * NT] = sj;
+    } else {
+      const uint4 v = R.load(j);
+      if (chunk_max<T>(v) >= thr) sj = esum_chunk_ge<T>(v, X, thr);
+    }
+    tmass += (double)sj;
+  }
+  return tmass;
+}
+
 // ---------------------------------------------------------------------------
-// One sampling row.  Every branch is uniform across the workgroup.
+// Sampling row, general form (rows with chunks past CAP): workgroup maximum,
+// masses relative to it, threshold, walk.
 // ---------------------------------------------------------------------------
 template <typename T, int NT, int CAP, bool VEC, bool FULL>
 __device__ __forceinline__ void row_sample(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
                                            Smem<NT>& S, float* csum) {
   constexpr int NW = NT / kWave;
+  float* cs = csum + threadIdx.x;
   const float tm = R.template maxima<false>();
   const float gm = wg_max<NW>(tm, S.red);
   if (!(A.T > 0.0f) || !(A.T < INFINITY) || !(gm > -INFINITY) || !(gm < INFINITY)) {
@@ -749,30 +868,275 @@ __device__ __forceinline__ void row_sample(Row<T, NT, CAP, VEC, FULL>& R, const 
     return;
   }
   Ex X;
-  X.init(gm, kLog2e / A.T);
-  double tmass = X.fma ? row_masses<true>(R, X, csum) : row_masses<false>(R, X, csum);
+  X.init_u(gm, kLog2e / A.T);
+  double tmass = X.fma ? row_masses<true>(R, X, cs) : row_masses<false>(R, X, cs);
   const bool kon = A.k >= 1 && (uint32_t)A.k < R.V, pon = A.p < 1.0f;
   if (!kon && !pon) {
-    cdf_walk(R, csum, tmass, false, -INFINITY, X, A.u, S, out);
+    cdf_walk<true>(R, tmass, cs, [&](int j) { return esum_chunk<T>(R.load(j), X); },
+                   [&](float x) { return X.e(x); }, A.u, S, out);
     return;
   }
   const double Z = wg_sum<NW>(tmass, S.red);
   float thr;
   if (!find_threshold<NT, T>(R, tm, X, Z, kon, A.k, pon, A.p, S, &thr))
     thr = select_exact<NW, T>(R, X, Z, kon, A.k, pon, A.p, S.red);
-  tmass = 0.0;
+  tmass = masked_masses(R, X, thr, cs);
+  cdf_walk<false>(R, tmass, cs,
+                  [&](int j) {
+                    const uint4 v = R.load(j);
+                    return chunk_max<T>(v) >= thr ? esum_chunk_ge<T>(v, X, thr) : 0.0f;
+                  },
+                  [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, A.u, S, out);
+}
+
+// ---------------------------------------------------------------------------
+// Sampling row held entirely in registers (no chunk is streamed):
+//   1. chunk maxima and the wave maximum; the chunk masses relative to the
+//      wave maximum (no workgroup maximum needed yet) and the wave total;
+//   2. one barrier; every wave derives the row maximum and converts the wave
+//      totals into the row's reference.
+// Without top-k / top-p the wave totals locate the crossing wave, which finds
+// the column, lane and element from its chunk masses (scaled by one factor).
+// With a filter, a candidate window bounded by a histogram of the thread
+// maxima is collected; a window of at most 64 elements is thresholded by every
+// wave (same result everywhere, so no broadcast barrier) and wave 0 walks the
+// kept elements in index order.  Larger windows take the general path.
+// ---------------------------------------------------------------------------
+template <int NW>
+__device__ __forceinline__ float lds_max(const float* v) {
+  const int lane = threadIdx.x & 63;
+  return wave_max(lane < NW ? v[lane] : -INFINITY);
+}
+
+
+
+// Window of nw <= 64 candidates in S.wkey: top-k / top-p threshold (order key
+// of the value), computed by the calling wave.  Returns false when the window
+// does not reach the top-p mass.  Also returns the wave's lanes in descending
+// value order (key) and their masses (e).
+template <int NT>
+__device__ __forceinline__ bool small_window(Smem<NT>& S, int nw, bool kon, int32_t k, bool pon, float p,
+                                             double Z, const Ex& X, uint32_t* tkey, uint64_t* key, float* e) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t mine = lane < nw ? S.wkey[lane] : 0ull;
+  // descending rank (keys are unique), then the key of rank `lane`
+  int rank = 0;
+  for (int q = 0; q < nw; ++q) {
+    const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
+    rank += other > mine ? 1 : 0;
+  }
+  // permute through ds_bpermute: lane `rank` receives `mine`
+  const int src = lane < nw ? rank : 63;
+  uint32_t lo = 0, hi = 0;
+  {
+    // invert the permutation: lane r needs the lane q with rank(q) == r
+    int from = 0;
+    for (int q = 0; q < nw; ++q) from = __builtin_amdgcn_readlane(src, q) == lane ? q : from;
+    lo = (uint32_t)__builtin_amdgcn_ds_bpermute(from << 2, (int)(mine & 0xffffffffu));
+    hi = (uint32_t)__builtin_amdgcn_ds_bpermute(from << 2, (int)(mine >> 32));
+  }
+  const uint64_t kk64 = lane < nw ? (((uint64_t)hi << 32) | lo) : 0ull;
+  const uint32_t kx = (uint32_t)(kk64 >> 32);
+  const float ev = lane < nw ? X.e(okey_inv(kx)) : 0.0f;
+  const double pre = wave_incl_scan((double)ev, lane);  // prefix in descending order
+  double ZK = Z;
+  int limit = nw;
+  uint32_t th = 0u;  // keep x with key >= th
+  if (kon) {
+    const uint32_t kk = (uint32_t)__builtin_amdgcn_readlane((int)kx, (k <= nw ? k : nw) - 1);
+    limit = __popcll(__ballot(lane < nw && kx >= kk));
+    th = kk;
+    ZK = readlane_d(pre, limit - 1);
+  }
+  if (pon) {
+    const uint64_t hit = __ballot(lane < limit && pre >= (double)p * ZK);
+    if (!hit) return false;
+    th = (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)hit) - 1);
+  }
+  *tkey = th;
+  *key = kk64;
+  *e = ev;
+  return true;
+}
+
+template <typename T, int NT, int CAP, bool VEC, bool FULL>
+__device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
+                                                 Smem<NT>& S, float* csum) {
+  constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  float* cs = csum + t;
+  const bool kon = A.k >= 1 && (uint32_t)A.k < R.V, pon = A.p < 1.0f;
+  if (t < kBins) {
+    S.hcnt[t] = 0;
+    S.hmass[t] = 0.0f;
+  }
+  if (t == 0) S.wn = 0;
+
+  const bool tvalid = A.T > 0.0f && A.T < INFINITY;
+  const float c = tvalid ? kLog2e / A.T : 1.0f;
+  // NaN-propagating maxima (v_maximum3, no operand canonicalisation); a wave
+  // holding a NaN (sampled as -inf) redoes its maxima ignoring NaN.
+  float tm = R.template maxima<true>();
+  float wm = wave_maximum(tm);
+  if (wm != wm) {
 #pragma unroll
-  for (int j = 0; j < CAP; ++j) {
-    float sj = 0.0f;
-    if (R.has(j) && R.cm.get(j) >= thr) sj = esum_chunk_ge<T>(R.load(j), X, thr);
-    csum[j * NT + threadIdx.x] = sj;
-    tmass += (double)sj;
+    for (int j = 0; j < CAP; ++j) launder(R.d[j]);  // no unpacked value shared with the first pass
+    tm = R.template maxima<false>();
+    wm = wave_max(tm);
   }
-  for (int j = CAP; j < R.nstream(); ++j) {
-    const uint4 v = R.load(j);
-    if (chunk_max<T>(v) >= thr) tmass += (double)esum_chunk_ge<T>(v, X, thr);
+  Ex Xw;  // this wave's shift
+  Xw.init_u(wm, c);
+  double tmass = 0.0;
+  if (tvalid) tmass = Xw.fma ? row_masses<true>(R, Xw, cs) : row_masses<false>(R, Xw, cs);
+  {
+    const double ws = wave_sum(tmass);
+    if (lane == 0) {
+      S.wtot[wid] = ws;
+      S.wmax[wid] = wm;
+    }
   }
-  cdf_walk(R, csum, tmass, true, thr, X, A.u, S, out);
+  __syncthreads();
+  const float gm = lds_max<NW>(S.wmax);
+  if (!tvalid || !(gm > -INFINITY) || !(gm < INFINITY)) {
+    const int32_t id = row_argmax<NW, T>(R, tm, gm, S.red);
+    if (t == 0) *out = id;
+    return;
+  }
+  Ex X;
+  X.init_u(gm, c);
+  double sw = 0.0;  // wave masses in the row's reference
+  if (lane < NW) {
+    Ex Xq;
+    Xq.init(S.wmax[lane], c);
+    sw = S.wtot[lane] * (double)shift_ratio(Xq, X);
+  }
+
+  if (!kon && !pon) {
+    int wstar;
+    double base;
+    const double U = cross_wave<NW>(sw, A.u, &wstar, &base);
+    if (wid != wstar) return;
+    const double fw = (double)shift_ratio(Xw, X);  // this wave's masses -> the row's
+    wave_walk<true>(R, cs, fw, base, U, [&](int) { return 0.0f; }, [&](float x) { return Xw.e(x); }, out);
+    return;
+  }
+  const double Z = wave_sum(sw);
+
+  // ---- top-k / top-p: candidate window from the chunk maxima -------------
+  // Histogram by y = log2(mass) of the two largest chunk maxima of each
+  // thread (distinct elements): their count (top-k) or mass (top-p) at or
+  // above a bin floor bounds that of the elements from below, so the first
+  // bin reaching k or p*Z bounds the threshold from below.  Two per thread
+  // catch most rows whose heaviest elements share a thread.
+  float yc[CAP];
+  {
+    typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
+    cmv.load(R.cmx);
+    float y1 = -INFINITY, y2 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      yc[j] = R.has(j) ? X.y(cmv.get(j)) : -INFINITY;
+      y2 = fmaxf(y2, fminf(y1, yc[j]));
+      y1 = fmaxf(y1, yc[j]);
+    }
+    if (y1 >= kYMin) {
+      if (kon) atomicAdd(&S.hcnt[ybin(y1)], 1);
+      else atomicAdd(&S.hmass[ybin(y1)], ex2c(y1));
+    }
+    if (y2 >= kYMin) {
+      if (kon) atomicAdd(&S.hcnt[ybin(y2)], 1);
+      else atomicAdd(&S.hmass[ybin(y2)], ex2c(y2));
+    }
+  }
+  __syncthreads();
+  int bin;
+  {
+    const int pc = wave_incl_scan_i(S.hcnt[lane], lane);
+    const double pm = wave_incl_scan((double)S.hmass[lane], lane);
+    const uint64_t bal = __ballot(kon ? (pc >= A.k) : (pm >= (double)A.p * Z * kBinMargin));
+    bin = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
+  }
+  if (bin >= 0) {
+    // Candidates: elements with y >= lo_y, from the chunks whose maximum
+    // reaches it.  Count, reserve one range of the window per wave, write.
+    const float lo_y = bin_floor(bin);
+    uint32_t km = 0;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (yc[j] >= lo_y) km |= 1u << j;
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (km & (1u << j)) {
+        uint4 v = R.d[j];
+        launder(v);
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) n += X.y(Elem<T>::get(v, i)) >= lo_y ? 1 : 0;
+      }
+    const int incl_n = wave_incl_scan_i(n, lane);
+    const int wtot = __builtin_amdgcn_readlane(incl_n, 63);
+    if (wtot > 0) {
+      int base = 0;
+      if (lane == 63) base = atomicAdd(&S.wn, wtot);
+      int pos = __builtin_amdgcn_readlane(base, 63) + incl_n - n;
+#pragma unroll
+      for (int j = 0; j < CAP; ++j)
+        if (km & (1u << j)) {
+          uint4 v = R.d[j];
+          launder(v);
+#pragma unroll
+          for (int i = 0; i < EPV; ++i) {
+            const float x = Elem<T>::get(v, i);
+            if (X.y(x) >= lo_y) {
+              if (pos < Smem<NT>::kWin)
+                S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
+              ++pos;
+            }
+          }
+        }
+    }
+  }
+  __syncthreads();
+  const int nw = bin >= 0 ? uni(S.wn) : 0x7fffffff;
+  if (nw <= kWave) {
+    // The window reaches the top-k count / top-p mass (bin test above), so
+    // wave 0 finishes the row alone.
+    if (wid != 0) return;
+    uint32_t tkey;
+    uint64_t key;
+    float e;
+    if (!small_window<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &tkey, &key, &e)) tkey = 0u;  // unreachable
+    // walk the kept elements (key >= tkey) in ascending index order
+    const bool in = lane < nw && (uint32_t)(key >> 32) >= tkey;
+    const uint32_t idx = 0xffffffffu - (uint32_t)(key & 0xffffffffu);
+    const float ek = in ? e : 0.0f;
+    const uint64_t inb = __ballot(in);
+    double pre = 0.0;  // mass of kept elements with index <= mine
+    for (uint64_t m = inb; m; m &= m - 1) {
+      const int q = __ffsll((unsigned long long)m) - 1;
+      const uint32_t iq = (uint32_t)__builtin_amdgcn_readlane((int)idx, q);
+      if (iq <= idx) pre += (double)readlane_f(ek, q);
+    }
+    const int last = wave_max_i(in ? (int)idx : -1);
+    const double total = readlane_d(pre, __ffsll((unsigned long long)__ballot(in && (int)idx == last)) - 1);
+    float u = A.u;
+    asm volatile("" : "+s"(u));
+    const double U = (double)u * total;
+    const int pick = wave_min_i(in && ek > 0.0f && pre > U ? (int)idx : 0x7fffffff);
+    int id = pick;
+    if (pick == 0x7fffffff) id = wave_max_i(in && ek > 0.0f ? (int)idx : -1);
+    if (lane == 0) *out = id < 0 ? last : id;
+    return;
+  }
+  // ---- general path: larger windows, exact search -------------------------
+  float thr;
+  bool ok = false;
+  if (bin >= 0 && nw <= Smem<NT>::kWin) ok = window_threshold<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &thr);
+  if (!ok) thr = select_exact<NW, T>(R, X, Z, kon, A.k, pon, A.p, S.red);
+  tmass = masked_masses(R, X, thr, cs);
+  cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; }, [&](float x) { return x >= thr ? X.e(x) : 0.0f; },
+                  A.u, S, out);
 }
 
 // One workgroup per output row b (grid = B_out).  WPE waves per SIMD: 8 lets two
@@ -783,6 +1147,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void sampler_kernel(SampleParams P) {
   __shared__ Smem<NT> S;
   __shared__ float csum[GREEDY ? 1 : NT * CAP];  // chunk masses, [j][thread]
+  __shared__ uint32_t cmax[NT * Row<T, NT, CAP, VEC, FULL>::kCmWords];  // chunk maxima, [thread][j]
   int64_t nrows = P.B_out;
   if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
   const int64_t b = blockIdx.x;
@@ -795,9 +1160,10 @@ void sampler_kernel(SampleParams P) {
   RowArgs A{};
   if (!GREEDY) A = row_args(P, r);
   Row<T, NT, CAP, VEC, FULL> R;
-  R.init(P.logits, r, P.ld, P.V);
+  R.init(P.logits, r, P.ld, P.V, cmax);
   R.fetch();
   if (GREEDY) row_greedy(R, &P.out[b], S);
+  else if (R.nstream() <= CAP) row_sample_fused(R, A, &P.out[b], S, csum);
   else row_sample(R, A, &P.out[b], S, csum);
 }
 
