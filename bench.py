@@ -14,6 +14,18 @@ Prints one JSON line (metric / value / roofline / cpu_baseline ...).
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                   [--no-cpu-baseline]
 Workloads: sample_huginn (default), sample_ouro, gate_cdb, cdb_mixed_depth.
+
+HBM traffic per launch (the roofline's "traffic" field) comes from two
+rocprofv3 counter runs of the probe mode, then the summary mode:
+
+  rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o run -- python3 bench.py --traffic-probe
+  rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o run -- python3 bench.py --traffic-probe
+  python3 bench.py --traffic-summary OUT/fetch OUT/write
+
+The probe launches the workload's kernel on rotating buffers plus a plain
+device-to-device copy of known size; the summary scales each counter by the
+copy's ratio (bytes moved / counter reading) and writes
+profiles/traffic_<workload>.json.
 """
 from __future__ import annotations
 
@@ -40,7 +52,56 @@ def _parse():
     ap.add_argument("--nbuf", type=int, default=0, help="logits buffers rotated (0: auto, > 512 MB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU baseline sample (0: auto)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="launch the kernel and a calibration copy for rocprofv3 --pmc, print nothing else")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 --pmc runs of --traffic-probe")
     return ap.parse_args()
+
+
+COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written
+PROBE_LAUNCHES = 10
+
+
+def _pmc_per_dispatch(outdir: str, counter: str):
+    """Average counter value (KiB, as rocprofv3 reports FETCH_SIZE/WRITE_SIZE)
+    per dispatch of the sampler/gate kernels and of the calibration copy."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {outdir}")
+    kern, copy = [], []
+    with open(files[0]) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            name, v = r["Kernel_Name"], float(r["Counter_Value"])
+            if "lsg::" in name:
+                kern.append((name, v))
+            elif "copyBuffer" in name or "elementwise" in name and "copy" in name:
+                copy.append(v)
+    if not kern or not copy:
+        raise SystemExit(f"{outdir}: kernel or calibration copy dispatches missing")
+    names = sorted({n for n, _ in kern})
+    return names, sum(v for _, v in kern) / len(kern), max(copy)
+
+
+def _traffic_summary(a):
+    kn, fk, fc = _pmc_per_dispatch(a.traffic_summary[0], "FETCH_SIZE")
+    _, wk, wc = _pmc_per_dispatch(a.traffic_summary[1], "WRITE_SIZE")
+    ff, fw = COPY_BYTES / (fc * 1024.0), COPY_BYTES / (wc * 1024.0)
+    fetch_b, write_b = fk * 1024.0 * ff, wk * 1024.0 * fw
+    out = {"workload": a.workload, "kernels": kn,
+           "fetch_kib_per_dispatch": fk, "write_kib_per_dispatch": wk,
+           "copy_fetch_kib": fc, "copy_write_kib": wc, "copy_bytes": COPY_BYTES,
+           "fetch_scale": ff, "write_scale": fw,
+           "traffic_bytes_per_launch": fetch_b + write_b}
+    path = os.path.join(ROOT, "profiles", f"traffic_{a.workload}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 def _traffic_from_profiles(workload: str):
@@ -97,8 +158,22 @@ def _cpu_baseline_sampling(wl, rows: int):
     return rows / dt, threads
 
 
+def _probe(torch, launch, dev):
+    for i in range(PROBE_LAUNCHES):
+        launch(i)
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def main():
     a = _parse()
+    if a.traffic_summary:
+        _traffic_summary(a)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {a.gpus}); the sampler shards rows across GPUs "
               "with no exchange, so run one process per GPU.", file=sys.stderr)
@@ -112,6 +187,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     K, W = a.steps, a.warmup
+    if a.traffic_probe:  # eager launches for the counter runs; no timing, no output
+        K, W = PROBE_LAUNCHES, 0
 
     if a.workload in ("sample_huginn", "sample_ouro", "cdb_mixed_depth"):
         if a.workload == "sample_huginn":
@@ -135,6 +212,9 @@ def main():
         def launch(i):
             pkg.sample_rows(bufs[i % nbuf], T, Kt, P, U, out=outs[i % nbuf])
 
+        if a.traffic_probe:
+            _probe(torch, launch, dev)
+            return
         secs = _time_graph(torch, launch, K, W)
         n_params = 2 + (Kt is not None)  # temperature, top_p (+ top_k) per row
         alg = wlmod.algorithmic_bytes_sampling(B, V, x0.element_size(), n_params)
@@ -142,7 +222,7 @@ def main():
         per_launch = secs / K
         cpu = None
         if not a.no_cpu_baseline:
-            rows = a.cpu_rows or min(B, 256)
+            rows = a.cpu_rows or B
             v, cores = _cpu_baseline_sampling(wl, rows)
             cpu = {"value": v, "unit": "rows/s", "cores": cores, "kind": "port",
                    "sample": f"first {rows} rows of the same {B}x{V} workload, float64 C oracle, 1 thread"}
@@ -182,6 +262,9 @@ def main():
         def launch(i):
             gate.exit_signal_compact(hs[i % nset], F, i % 4)
 
+        if a.traffic_probe:
+            _probe(torch, launch, dev)
+            return
         secs = _time_graph(torch, launch, K, W)
         per = secs / K
         alg = wlmod.algorithmic_bytes_gate(B, H)
