@@ -38,7 +38,8 @@ constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
 // Margin on the top-p histogram test: the bin is chosen where the float sum of
 // the binned maxima reaches p*Z*(1 + 2^-10), so the window (a superset of those
 // maxima, summed in double) always reaches p*Z despite the rounding of the
-// float atomic additions (at most 2048 terms: error < 2048 * 2^-24 < 2^-10).
+// float sums (at most 2048 terms: < 2^-13 relative) and of the per-wave
+// reference shifts (< 2^-17 relative per term).
 constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
 
 struct SampleParams {
@@ -101,14 +102,13 @@ struct Ex {
 // 2^(shift(a) - shift(b)): converts masses relative to a's maximum into masses
 // relative to b's (a.gm <= b.gm, same c).  The shift of the fma form is the
 // float -nb, that of the other form gm * c.
-__device__ __forceinline__ float shift_ratio(const Ex& a, const Ex& b) {
-  float d;
-  if (a.fma && b.fma) d = b.nb - a.nb;
-  else if (a.fma) d = __builtin_fmaf(-b.gm, b.c, -a.nb);
-  else if (b.fma) d = __builtin_fmaf(a.gm, a.c, b.nb);
-  else d = (a.gm - b.gm) * a.c;
-  return ex2c(d);
+__device__ __forceinline__ float shift_diff(const Ex& a, const Ex& b) {
+  if (a.fma && b.fma) return b.nb - a.nb;
+  if (a.fma) return __builtin_fmaf(-b.gm, b.c, -a.nb);
+  if (b.fma) return __builtin_fmaf(a.gm, a.c, b.nb);
+  return (a.gm - b.gm) * a.c;
 }
+__device__ __forceinline__ float shift_ratio(const Ex& a, const Ex& b) { return ex2c(shift_diff(a, b)); }
 
 template <int EPV>
 __device__ __forceinline__ float tree_sum(float (&e)[EPV]) {
@@ -264,6 +264,10 @@ struct Smem {
   float wmax[NW];   // per-wave maxima
   int hcnt[kBins];
   float hmass[kBins];
+  uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass as float bits)
+  int fcnt[kBins];         // refinement bins: member count
+  double fmass[kBins];     // refinement bins: member mass
+  uint32_t kmin;           // smallest order key in the candidate window
   uint64_t wkey[kWin];    // candidate window (unsorted)
   uint64_t sorted[kWin];  // candidate window in descending key order
   int wn;
@@ -960,6 +964,120 @@ __device__ __forceinline__ bool small_window(Smem<NT>& S, int nw, bool kon, int3
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Exact top-k (count target k) or top-p (mass target p * ZK) threshold by radix
+// refinement in order-key space (key = okey(x) >> SH).  Members are the non-NaN
+// elements with key >= klo; the boundary lies among them.  Each level splits
+// the bracket [lo, hi) of keys that holds the boundary into 64 bins of 2^sh
+// keys, counts the members per bin (and sums their masses in double), and
+// scans from the top with the totals above the bracket to pick the bin that
+// holds the boundary.  A bin of one key is the answer (ties are kept); a bin
+// of at most 64 members is ranked by wave 0.  Returns false when the members
+// never reach the target.  All waves of the workgroup call it together.
+// ---------------------------------------------------------------------------
+template <int NT, typename T, class R_>
+__device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, bool kon, int32_t k, float p,
+                                                 uint32_t klo, Smem<NT>& S, uint32_t* thr_key) {
+  constexpr int SH = KeyShift<T>::value, EPV = Elem<T>::EPV;
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  uint32_t lo = klo, hi = (okey(X.gm) >> SH) + 1u;  // keys in [lo, hi)
+  int above_c = 0;
+  double above_m = 0.0;
+  const double target = (double)p * ZK;
+  for (;;) {
+    if (hi <= lo) return false;
+    int sh = 0;
+    while (((hi - lo - 1u) >> sh) >= (uint32_t)kBins) ++sh;
+    if (t < kBins) {
+      S.fcnt[t] = 0;
+      S.fmass[t] = 0.0;
+    }
+    if (t == 0) S.wn = 0;
+    __syncthreads();
+    const uint32_t lo_ = lo, hi_ = hi;
+    auto member = [&](float x, uint32_t* key) {
+      *key = okey(x) >> SH;
+      return x == x && *key >= lo_ && *key < hi_;
+    };
+    const float xlo = okey_inv(lo << SH);  // smallest value with key lo (NaN for lo == 0)
+    auto keep = [&](float m) { return lo == 0u || m >= xlo; };
+    R.each_kept_mem(keep,
+                    [&](int, const uint4& v, float) {
+#pragma unroll 1
+                      for (int i = 0; i < EPV; ++i) {
+                        const float x = Elem<T>::get(v, i);
+                        uint32_t key;
+                        if (member(x, &key)) {
+                          const int b = (int)((hi_ - 1u - key) >> sh);
+                          atomicAdd(&S.fcnt[b], 1);
+                          if (!kon) atomicAdd(&S.fmass[b], (double)X.e(x));
+                        }
+                      }
+                    });
+    __syncthreads();
+    const int cb = S.fcnt[lane];
+    const double mb = kon ? 0.0 : S.fmass[lane];
+    const int ic = wave_incl_scan_i(cb, lane);
+    const double im = wave_incl_scan(mb, lane);
+    const uint64_t bal = __ballot(kon ? (above_c + ic >= k) : (above_m + im >= target));
+    if (!bal) return false;
+    const int bs = __ffsll((unsigned long long)bal) - 1;
+    const int cnt = __builtin_amdgcn_readlane(cb, bs);
+    above_c += __builtin_amdgcn_readlane(ic - cb, bs);
+    above_m += readlane_d(im - mb, bs);
+    const uint32_t nhi = hi - ((uint32_t)bs << sh);
+    const uint32_t nlo = nhi - lo > (1u << sh) ? nhi - (1u << sh) : lo;
+    __syncthreads();  // every wave has read the bins
+    lo = nlo;
+    hi = nhi;
+    if (hi - lo == 1u) {
+      *thr_key = lo;
+      return true;
+    }
+    if (cnt > kWave) continue;
+    // Final: rank the boundary bin's members (at most 64) in wave 0.
+    const float xlo2 = okey_inv(lo << SH);
+    R.each_kept_mem([&](float m) { return lo == 0u || m >= xlo2; },
+                    [&](int j, const uint4& v, float) {
+#pragma unroll 1
+                      for (int i = 0; i < EPV; ++i) {
+                        const float x = Elem<T>::get(v, i);
+                        const uint32_t key = okey(x) >> SH;
+                        if (x == x && key >= lo && key < hi) {
+                          const int pos = atomicAdd(&S.wn, 1);
+                          if (pos < kWave)
+                            S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
+                        }
+                      }
+                    });
+    __syncthreads();
+    if (wid == 0) {
+      const int n = min(uni(S.wn), kWave);
+      const uint64_t mine = lane < n ? S.wkey[lane] : 0ull;
+      const float e = (lane < n && !kon) ? X.e(okey_inv((uint32_t)(mine >> 32))) : 0.0f;
+      int rank = 0;      // members above mine
+      double pre = 0.0;  // mass of members at or above mine (keys are unique)
+      for (int q = 0; q < n; ++q) {
+        const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
+                               (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
+        rank += other > mine ? 1 : 0;
+        if (other >= mine) pre += (double)readlane_f(e, q);
+      }
+      const bool hit = lane < n && (kon ? (above_c + rank + 1 >= k) : (above_m + pre >= target));
+      // the hit with the smallest rank is the boundary element
+      const int r = wave_min_i(hit ? rank : 0x7fffffff);
+      const uint64_t who = __ballot(hit && rank == r);
+      if (lane == 0) S.pick = who ? (int)(__builtin_amdgcn_readlane((int)(mine >> 32), __ffsll((unsigned long long)who) - 1)) : 0;
+      if (lane == 0) S.wn = who ? 1 : 0;
+    }
+    __syncthreads();
+    const bool found = uni(S.wn) != 0;
+    *thr_key = (uint32_t)uni(S.pick) >> SH;
+    __syncthreads();
+    return found;
+  }
+}
+
 template <typename T, int NT, int CAP, bool VEC, bool FULL>
 __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
                                                  Smem<NT>& S, float* csum) {
@@ -967,11 +1085,11 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
   float* cs = csum + t;
   const bool kon = A.k >= 1 && (uint32_t)A.k < R.V, pon = A.p < 1.0f;
-  if (t < kBins) {
-    S.hcnt[t] = 0;
-    S.hmass[t] = 0.0f;
+  if (t == 0) {
+    S.wn = 0;
+    S.kmin = 0xffffffffu;
   }
-  if (t == 0) S.wn = 0;
+  if (kon || pon) S.wh[wid][lane] = 0u;  // this wave's histogram (LDS ops of a wave stay in order)
 
   const bool tvalid = A.T > 0.0f && A.T < INFINITY;
   const float c = tvalid ? kLog2e / A.T : 1.0f;
@@ -996,6 +1114,30 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       S.wmax[wid] = wm;
     }
   }
+  if (kon || pon) {
+    // Histogram, relative to this wave's maximum, of the two largest chunk
+    // maxima of each thread (distinct elements): count (top-k) or mass
+    // (top-p) per bin of y = log2(mass).  Merged into the row's histogram
+    // after the barrier.
+    typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
+    cmv.load(R.cmx);
+    float y1 = -INFINITY, y2 = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      const float y = R.has(j) ? Xw.y(cmv.get(j)) : -INFINITY;
+      y2 = fmaxf(y2, fminf(y1, y));
+      y1 = fmaxf(y1, y);
+    }
+    uint32_t* h = S.wh[wid];
+    if (y1 >= kYMin) {
+      if (kon) atomicAdd(&h[ybin(y1)], 1u);
+      else atomicAdd(reinterpret_cast<float*>(&h[ybin(y1)]), ex2c(y1));
+    }
+    if (y2 >= kYMin) {
+      if (kon) atomicAdd(&h[ybin(y2)], 1u);
+      else atomicAdd(reinterpret_cast<float*>(&h[ybin(y2)]), ex2c(y2));
+    }
+  }
   __syncthreads();
   const float gm = lds_max<NW>(S.wmax);
   if (!tvalid || !(gm > -INFINITY) || !(gm < INFINITY)) {
@@ -1006,10 +1148,15 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   Ex X;
   X.init_u(gm, c);
   double sw = 0.0;  // wave masses in the row's reference
+  float fq = 0.0f;  // lane q < NW: wave q's mass factor and shift in bins
+  int sq = kBins;
   if (lane < NW) {
     Ex Xq;
     Xq.init(S.wmax[lane], c);
-    sw = S.wtot[lane] * (double)shift_ratio(Xq, X);
+    const float d = shift_diff(Xq, X);  // <= 0
+    fq = ex2c(d);
+    sw = S.wtot[lane] * (double)fq;
+    sq = d > -32.0f ? (int)__builtin_ceilf(-2.0f * d + 0x1p-10f) : kBins;
   }
 
   if (!kon && !pon) {
@@ -1024,38 +1171,36 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   const double Z = wave_sum(sw);
 
   // ---- top-k / top-p: candidate window from the chunk maxima -------------
-  // Histogram by y = log2(mass) of the two largest chunk maxima of each
-  // thread (distinct elements): their count (top-k) or mass (top-p) at or
-  // above a bin floor bounds that of the elements from below, so the first
-  // bin reaching k or p*Z bounds the threshold from below.  Two per thread
-  // catch most rows whose heaviest elements share a thread.
+  // The count (top-k) or mass (top-p) of distinct elements at or above a bin
+  // floor bounds that of all elements from below, so the first bin reaching k
+  // or p*Z bounds the threshold from below.  Row bin r gathers bin r - s_q of
+  // every wave q: a wave bin's contents sit at least s_q/2 lower in the row's
+  // reference (s_q = ceil(2 * shift), with a margin for the rounding of y).
+  int bin;
+  {
+    int pc = 0;
+    float pmf = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      const int s = __builtin_amdgcn_readlane(sq, q);
+      const int idx = lane - s;
+      if (idx >= 0) {
+        const uint32_t v = S.wh[q][idx];
+        if (kon) pc += (int)v;
+        else pmf = __builtin_fmaf(__uint_as_float(v), readlane_f(fq, q), pmf);
+      }
+    }
+    const int pcs = wave_incl_scan_i(pc, lane);
+    const double pm = wave_incl_scan((double)pmf, lane);
+    const uint64_t bal = __ballot(kon ? (pcs >= A.k) : (pm >= (double)A.p * Z * kBinMargin));
+    bin = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
+  }
   float yc[CAP];
   {
     typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
     cmv.load(R.cmx);
-    float y1 = -INFINITY, y2 = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      yc[j] = R.has(j) ? X.y(cmv.get(j)) : -INFINITY;
-      y2 = fmaxf(y2, fminf(y1, yc[j]));
-      y1 = fmaxf(y1, yc[j]);
-    }
-    if (y1 >= kYMin) {
-      if (kon) atomicAdd(&S.hcnt[ybin(y1)], 1);
-      else atomicAdd(&S.hmass[ybin(y1)], ex2c(y1));
-    }
-    if (y2 >= kYMin) {
-      if (kon) atomicAdd(&S.hcnt[ybin(y2)], 1);
-      else atomicAdd(&S.hmass[ybin(y2)], ex2c(y2));
-    }
-  }
-  __syncthreads();
-  int bin;
-  {
-    const int pc = wave_incl_scan_i(S.hcnt[lane], lane);
-    const double pm = wave_incl_scan((double)S.hmass[lane], lane);
-    const uint64_t bal = __ballot(kon ? (pc >= A.k) : (pm >= (double)A.p * Z * kBinMargin));
-    bin = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
+    for (int j = 0; j < CAP; ++j) yc[j] = R.has(j) ? X.y(cmv.get(j)) : -INFINITY;
   }
   if (bin >= 0) {
     // Candidates: elements with y >= lo_y, from the chunks whose maximum
@@ -1080,6 +1225,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       int base = 0;
       if (lane == 63) base = atomicAdd(&S.wn, wtot);
       int pos = __builtin_amdgcn_readlane(base, 63) + incl_n - n;
+      uint32_t kmn = 0xffffffffu;
 #pragma unroll
       for (int j = 0; j < CAP; ++j)
         if (km & (1u << j)) {
@@ -1089,12 +1235,16 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
           for (int i = 0; i < EPV; ++i) {
             const float x = Elem<T>::get(v, i);
             if (X.y(x) >= lo_y) {
+              const uint32_t kx = okey(x);
               if (pos < Smem<NT>::kWin)
-                S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
+                S.wkey[pos] = ((uint64_t)kx << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
               ++pos;
+              kmn = min(kmn, kx);
             }
           }
         }
+      kmn = (uint32_t)wave_min_i((int)(kmn ^ 0x80000000u)) ^ 0x80000000u;
+      if (lane == 0) atomicMin(&S.kmin, kmn);
     }
   }
   __syncthreads();
@@ -1129,11 +1279,35 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     if (lane == 0) *out = id < 0 ? last : id;
     return;
   }
-  // ---- general path: larger windows, exact search -------------------------
-  float thr;
-  bool ok = false;
-  if (bin >= 0 && nw <= Smem<NT>::kWin) ok = window_threshold<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &thr);
-  if (!ok) thr = select_exact<NW, T>(R, X, Z, kon, A.k, pon, A.p, S.red);
+  // ---- larger windows: ranked by the workgroup (<= 512 candidates), else an
+  // exact refinement over the window (or over the row when there is no bound)
+  if (bin >= 0 && nw <= Smem<NT>::kWin) {
+    float thr;
+    if (window_threshold<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &thr)) {
+      tmass = masked_masses(R, X, thr, cs);
+      cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; },
+                      [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, A.u, S, out);
+      return;
+    }
+  }
+  constexpr int SH = KeyShift<T>::value;
+  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH) : 0u;
+  uint32_t tk = 0;
+  bool ok;
+  if (kon) {
+    ok = refine_threshold<NT, T>(R, X, Z, true, A.k, 1.0f, klo, S, &tk);
+    if (ok && pon) {
+      const float thr_k = okey_inv(tk << SH);
+      double acc = 0.0;
+      R.each_kept_mem([&](float m) { return m >= thr_k; },
+                      [&](int, const uint4& v, float) { acc += (double)esum_chunk_ge<T>(v, X, thr_k); });
+      const double ZK = wg_sum<NW>(acc, S.red);
+      ok = refine_threshold<NT, T>(R, X, ZK, false, 0, A.p, tk, S, &tk);
+    }
+  } else {
+    ok = refine_threshold<NT, T>(R, X, Z, false, 0, A.p, klo, S, &tk);
+  }
+  const float thr = ok ? okey_inv(tk << SH) : select_exact<NW, T>(R, X, Z, kon, A.k, pon, A.p, S.red);
   tmass = masked_masses(R, X, thr, cs);
   cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; }, [&](float x) { return x >= thr ? X.e(x) : 0.0f; },
                   A.u, S, out);
