@@ -33,6 +33,10 @@
 namespace lsg {
 
 constexpr float kLog2e = 1.4426950408889634f;
+// Row shapes (the FULL template argument): rows of any length, streaming the
+// chunks past the register capacity; rows of at most NT*CAP chunks; rows of
+// exactly NT*CAP full chunks.
+constexpr int kStream = 0, kBounded = 2, kFull = 1;
 constexpr int kBins = 64;  // histogram of y = log2(e / e_max): bins of width 1/2
 constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
 // Margin on the top-p histogram test: the bin is chosen where the float sum of
@@ -109,6 +113,25 @@ __device__ __forceinline__ float shift_diff(const Ex& a, const Ex& b) {
   return (a.gm - b.gm) * a.c;
 }
 __device__ __forceinline__ float shift_ratio(const Ex& a, const Ex& b) { return ex2c(shift_diff(a, b)); }
+
+// Smallest float x with X.y(x) >= ly (X.y is monotone non-decreasing in x), so
+// that "X.y(x) >= ly" becomes one compare.  Starts from the algebraic inverse
+// and steps one float at a time (order keys) until the test flips.  ly and X
+// are wave-uniform.
+__device__ __forceinline__ float x_at_least(const Ex& X, float ly) {
+  float x = X.fma ? (ly - X.nb) / X.c : ly / X.c + X.gm;
+  x = uni(x);
+  if (X.y(x) >= ly) {
+    for (int i = 0; i < 64; ++i) {
+      const float xd = okey_inv(okey(x) - 1u);
+      if (!(X.y(xd) >= ly)) break;
+      x = xd;
+    }
+  } else {
+    for (int i = 0; i < 64 && !(X.y(x) >= ly); ++i) x = okey_inv(okey(x) + 1u);
+  }
+  return uni(x);
+}
 
 template <int EPV>
 __device__ __forceinline__ float tree_sum(float (&e)[EPV]) {
@@ -268,6 +291,8 @@ struct Smem {
   int fcnt[kBins];         // refinement bins: member count
   double fmass[kBins];     // refinement bins: member mass
   uint32_t kmin;           // smallest order key in the candidate window
+  float we[kWave];         // small window: masses
+  uint32_t widx[kWave];    // small window: vocabulary indices
   uint64_t wkey[kWin];    // candidate window (unsorted)
   uint64_t sorted[kWin];  // candidate window in descending key order
   int wn;
@@ -280,10 +305,10 @@ struct Smem {
 // consecutive chunks (w*L + j)*64 + lane (1 KiB of contiguous HBM), so the
 // index order is (wave, j, lane, element).  Chunks j < CAP stay in registers;
 // their maxima go to LDS.  Chunks j >= CAP (very long rows) are re-read on
-// every pass.  FULL: the row is exactly NT*CAP full chunks (every thread holds
+// every pass.  FULL (kFull = 1): the row is exactly NT*CAP full chunks (every thread holds
 // CAP chunks, no partial or padding chunk), so loads need no bounds checks.
 // ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC, bool FULL>
+template <typename T, int NT, int CAP, bool VEC, int FULL>
 struct Row {
   static constexpr int EPV = Elem<T>::EPV;
   using CM = ChunkMax<T, CAP>;
@@ -300,14 +325,17 @@ struct Row {
     base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)Elem<T>::kSize;
     V = (uint32_t)uni((uint32_t)Vv);
     const uint32_t NV = (V + EPV - 1) / EPV;
-    L = FULL ? CAP : (int)((NV + NT - 1) / NT);
+    L = FULL == kFull ? CAP : (int)((NV + NT - 1) / NT);
     c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)L * kWave + (threadIdx.x & 63);
   }
-  __device__ __forceinline__ bool has(int j) const { return FULL ? j < CAP : j < L; }
-  __device__ __forceinline__ int nstream() const { return FULL ? CAP : L; }  // chunks of this thread
+  __device__ __forceinline__ bool has(int j) const { return FULL == kFull ? j < CAP : j < L; }
+  // chunks of this thread (kBounded: at most CAP, so no chunk is streamed)
+  __device__ __forceinline__ int nstream() const {
+    return FULL == kFull ? CAP : FULL == kBounded ? min(L, CAP) : L;
+  }
   __device__ __forceinline__ uint32_t chunk_index(int j) const { return c0 + (uint32_t)j * kWave; }
   __device__ __forceinline__ uint4 load(int j) const {
-    if (FULL) return *reinterpret_cast<const uint4*>(base + chunk_index(j) * 16u);
+    if (FULL == kFull) return *reinterpret_cast<const uint4*>(base + chunk_index(j) * 16u);
     return load_chunk32<T, VEC>(base, chunk_index(j), V);
   }
   __device__ __forceinline__ uint32_t elem_index(int j, int i) const {
@@ -679,7 +707,7 @@ __device__ __forceinline__ int64_t source_row(const SampleParams& P, int64_t b, 
 // row maximum, so one pass finds both the maximum and whether NaN is present;
 // the chunk maxima then point at the chunk holding the first hit.
 // ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC, bool FULL>
+template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ void row_greedy(Row<T, NT, CAP, VEC, FULL>& R, int32_t* out, Smem<NT>& S) {
   constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
   const float tm = R.template maxima<true>();
@@ -716,7 +744,7 @@ __device__ __forceinline__ void row_greedy(Row<T, NT, CAP, VEC, FULL>& R, int32_
 // the chosen chunk is taken from registers, else re-read.  The owner lane
 // writes the id.
 // ---------------------------------------------------------------------------
-template <bool REG, typename T, int NT, int CAP, bool VEC, bool FULL, class CMass, class EMass>
+template <bool REG, typename T, int NT, int CAP, bool VEC, int FULL, class CMass, class EMass>
 __device__ __forceinline__ void wave_walk(Row<T, NT, CAP, VEC, FULL>& R, const float* cs, double fw, double base,
                                           double U, CMass&& chunk_mass, EMass&& elem_mass, int32_t* out) {
   constexpr int EPV = Elem<T>::EPV;
@@ -724,8 +752,7 @@ __device__ __forceinline__ void wave_walk(Row<T, NT, CAP, VEC, FULL>& R, const f
   int jstar = -1, jlast = 0;
   double jbase = base, cum = base, cum_last = base;
   float sme = 0.0f, slast = 0.0f;
-  auto column = [&](int j, float sj) {
-    const double col = wave_sum((double)sj) * fw;
+  auto column = [&](int j, double col, float sj) {
     if (col > 0.0) {
       jlast = j;
       slast = sj;
@@ -738,10 +765,23 @@ __device__ __forceinline__ void wave_walk(Row<T, NT, CAP, VEC, FULL>& R, const f
     }
     cum += col;
   };
+  {
+    // the register columns' masses first (independent reductions), then the scan
+    float sv[CAP];
+    double colv[CAP];
 #pragma unroll
-  for (int j = 0; j < CAP; ++j)
-    if (R.has(j)) column(j, cs[j * NT]);
-  for (int j = CAP; j < R.nstream(); ++j) column(j, chunk_mass(j));
+    for (int j = 0; j < CAP; ++j) {
+      sv[j] = R.has(j) ? cs[j * NT] : 0.0f;
+      colv[j] = uni(wave_sum((double)sv[j]) * fw);  // wave-uniform: scalar registers
+    }
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      if (R.has(j)) column(j, colv[j], sv[j]);
+  }
+  for (int j = CAP; j < R.nstream(); ++j) {
+    const float sj = chunk_mass(j);
+    column(j, wave_sum((double)sj) * fw, sj);
+  }
   if (jstar < 0) {
     jstar = jlast;
     jbase = cum_last;
@@ -762,11 +802,14 @@ __device__ __forceinline__ void wave_walk(Row<T, NT, CAP, VEC, FULL>& R, const f
   }
   if (lane != owner) return;
   const uint4 v = REG ? R.chunk(jstar) : R.load(jstar);
+  float ev[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) ev[i] = elem_mass(Elem<T>::get(v, i));
   double a = jbase + excl;
   int pick = -1, lastpos = -1;
-#pragma unroll 1
+#pragma unroll
   for (int i = 0; i < EPV; ++i) {
-    const double e = (double)elem_mass(Elem<T>::get(v, i)) * fw;
+    const double e = (double)ev[i] * fw;
     if (e > 0.0) {
       lastpos = i;
       a += e;
@@ -802,7 +845,7 @@ __device__ __forceinline__ double cross_wave(double sw, float u, int* wstar, dou
 
 // Full inverse-CDF walk with the masses in the row's reference: wave totals
 // through LDS (one barrier), crossing wave, then wave_walk.
-template <bool REG, typename T, int NT, int CAP, bool VEC, bool FULL, class CMass, class EMass>
+template <bool REG, typename T, int NT, int CAP, bool VEC, int FULL, class CMass, class EMass>
 __device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, double tmass, const float* cs,
                                          CMass&& chunk_mass, EMass&& elem_mass, float u, Smem<NT>& S,
                                          int32_t* out) {
@@ -820,7 +863,7 @@ __device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, double t
 
 // This thread's chunk masses (register chunks) -> cs[j * NT] in LDS and its
 // total mass (chunks past CAP included).
-template <bool FMA, typename T, int NT, int CAP, bool VEC, bool FULL>
+template <bool FMA, typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float* cs) {
   double tmass = 0.0;
 #pragma unroll
@@ -837,7 +880,7 @@ __device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, cons
 
 // Masked chunk masses (x >= thr, relative to X) -> cs and the total; chunks are
 // re-read from memory.
-template <typename T, int NT, int CAP, bool VEC, bool FULL>
+template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ double masked_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float thr, float* cs) {
   double tmass = 0.0;
 #pragma unroll 1
@@ -859,7 +902,7 @@ __device__ __forceinline__ double masked_masses(Row<T, NT, CAP, VEC, FULL>& R, c
 // Sampling row, general form (rows with chunks past CAP): workgroup maximum,
 // masses relative to it, threshold, walk.
 // ---------------------------------------------------------------------------
-template <typename T, int NT, int CAP, bool VEC, bool FULL>
+template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ void row_sample(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
                                            Smem<NT>& S, float* csum) {
   constexpr int NW = NT / kWave;
@@ -916,51 +959,49 @@ __device__ __forceinline__ float lds_max(const float* v) {
 
 // Window of nw <= 64 candidates in S.wkey: top-k / top-p threshold (order key
 // of the value), computed by the calling wave.  Returns false when the window
-// does not reach the top-p mass.  Also returns the wave's lanes in descending
-// value order (key) and their masses (e).
+// does not reach the top-p mass.  Also returns each lane's window entry (key)
+// and its mass (e).  Each lane counts the entries at or above its own and sums
+// their masses, reading the window with broadcast LDS loads (keys are unique).
 template <int NT>
 __device__ __forceinline__ bool small_window(Smem<NT>& S, int nw, bool kon, int32_t k, bool pon, float p,
                                              double Z, const Ex& X, uint32_t* tkey, uint64_t* key, float* e) {
   const int lane = threadIdx.x & 63;
-  const uint64_t mine = lane < nw ? S.wkey[lane] : 0ull;
-  // descending rank (keys are unique), then the key of rank `lane`
-  int rank = 0;
-  for (int q = 0; q < nw; ++q) {
-    const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
-                           (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
-    rank += other > mine ? 1 : 0;
+  const bool in = lane < nw;
+  const uint64_t mine = in ? S.wkey[lane] : 0ull;
+  const uint32_t kx = (uint32_t)(mine >> 32);
+  const float em = in ? X.e(okey_inv(kx)) : 0.0f;
+  S.we[lane] = em;
+  int cnt = 0;       // entries at or above mine
+  double pre = 0.0;  // their mass
+  for (int q0 = 0; q0 < nw; q0 += 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = q0 + i;
+      const uint64_t other = S.wkey[q];
+      const float eo = S.we[q];
+      const bool ge = q < nw && other >= mine;
+      cnt += ge ? 1 : 0;
+      pre += ge ? (double)eo : 0.0;
+    }
   }
-  // permute through ds_bpermute: lane `rank` receives `mine`
-  const int src = lane < nw ? rank : 63;
-  uint32_t lo = 0, hi = 0;
-  {
-    // invert the permutation: lane r needs the lane q with rank(q) == r
-    int from = 0;
-    for (int q = 0; q < nw; ++q) from = __builtin_amdgcn_readlane(src, q) == lane ? q : from;
-    lo = (uint32_t)__builtin_amdgcn_ds_bpermute(from << 2, (int)(mine & 0xffffffffu));
-    hi = (uint32_t)__builtin_amdgcn_ds_bpermute(from << 2, (int)(mine >> 32));
-  }
-  const uint64_t kk64 = lane < nw ? (((uint64_t)hi << 32) | lo) : 0ull;
-  const uint32_t kx = (uint32_t)(kk64 >> 32);
-  const float ev = lane < nw ? X.e(okey_inv(kx)) : 0.0f;
-  const double pre = wave_incl_scan((double)ev, lane);  // prefix in descending order
+  uint32_t th = 0u;  // keep values with key >= th
   double ZK = Z;
-  int limit = nw;
-  uint32_t th = 0u;  // keep x with key >= th
   if (kon) {
-    const uint32_t kk = (uint32_t)__builtin_amdgcn_readlane((int)kx, (k <= nw ? k : nw) - 1);
-    limit = __popcll(__ballot(lane < nw && kx >= kk));
-    th = kk;
-    ZK = readlane_d(pre, limit - 1);
+    const uint64_t b = __ballot(in && cnt == (k <= nw ? k : nw));  // the k-th largest
+    if (!b) return false;
+    th = (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)b) - 1);
+    ZK = wave_sum(in && kx >= th ? (double)em : 0.0);
   }
   if (pon) {
-    const uint64_t hit = __ballot(lane < limit && pre >= (double)p * ZK);
-    if (!hit) return false;
-    th = (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)hit) - 1);
+    const bool hit = in && kx >= th && pre >= (double)p * ZK;
+    const int r = wave_min_i(hit ? cnt : 0x7fffffff);
+    const uint64_t b = __ballot(hit && cnt == r);
+    if (!b) return false;
+    th = (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)b) - 1);
   }
   *tkey = th;
-  *key = kk64;
-  *e = ev;
+  *key = mine;
+  *e = em;
   return true;
 }
 
@@ -1078,7 +1119,7 @@ __device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, 
   }
 }
 
-template <typename T, int NT, int CAP, bool VEC, bool FULL>
+template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
                                                  Smem<NT>& S, float* csum) {
   constexpr int NW = NT / kWave, EPV = Elem<T>::EPV;
@@ -1139,6 +1180,9 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
   }
   __syncthreads();
+  // The rest of the row is short, latency-bound work: let it go ahead of the
+  // co-resident workgroup's streaming passes.
+  __builtin_amdgcn_s_setprio(2);
   const float gm = lds_max<NW>(S.wmax);
   if (!tvalid || !(gm > -INFINITY) || !(gm < INFINITY)) {
     const int32_t id = row_argmax<NW, T>(R, tm, gm, S.red);
@@ -1180,36 +1224,44 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   {
     int pc = 0;
     float pmf = 0.0f;
+    int sqs[NW];
+    float fqs[NW];
+    uint32_t v[NW];
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-      const int s = __builtin_amdgcn_readlane(sq, q);
-      const int idx = lane - s;
-      if (idx >= 0) {
-        const uint32_t v = S.wh[q][idx];
-        if (kon) pc += (int)v;
-        else pmf = __builtin_fmaf(__uint_as_float(v), readlane_f(fq, q), pmf);
-      }
+      sqs[q] = __builtin_amdgcn_readlane(sq, q);
+      fqs[q] = readlane_f(fq, q);
+    }
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {  // independent loads (clamped index), issued back to back
+      const int idx = lane - sqs[q];
+      v[q] = S.wh[q][idx < 0 ? 0 : idx];
+    }
+    if (kon) {
+#pragma unroll
+      for (int q = 0; q < NW; ++q) pc += lane >= sqs[q] ? (int)v[q] : 0;
+    } else {
+#pragma unroll
+      for (int q = 0; q < NW; ++q) pmf = __builtin_fmaf(__uint_as_float(v[q]), lane >= sqs[q] ? fqs[q] : 0.0f, pmf);
     }
     const int pcs = wave_incl_scan_i(pc, lane);
     const double pm = wave_incl_scan((double)pmf, lane);
     const uint64_t bal = __ballot(kon ? (pcs >= A.k) : (pm >= (double)A.p * Z * kBinMargin));
     bin = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
   }
-  float yc[CAP];
-  {
-    typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
-    cmv.load(R.cmx);
-#pragma unroll
-    for (int j = 0; j < CAP; ++j) yc[j] = R.has(j) ? X.y(cmv.get(j)) : -INFINITY;
-  }
   if (bin >= 0) {
-    // Candidates: elements with y >= lo_y, from the chunks whose maximum
-    // reaches it.  Count, reserve one range of the window per wave, write.
-    const float lo_y = bin_floor(bin);
+    // Candidates: elements with y at or above the bin floor (x >= xlo), from
+    // the chunks whose maximum reaches it.  Count, reserve one range of the
+    // window per wave, write.
+    const float xlo = x_at_least(X, bin_floor(bin));  // candidate: x >= xlo
     uint32_t km = 0;
+    {
+      typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
+      cmv.load(R.cmx);
 #pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (yc[j] >= lo_y) km |= 1u << j;
+      for (int j = 0; j < CAP; ++j)
+        if (R.has(j) && cmv.get(j) >= xlo) km |= 1u << j;
+    }
     int n = 0;
 #pragma unroll
     for (int j = 0; j < CAP; ++j)
@@ -1217,7 +1269,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
         uint4 v = R.d[j];
         launder(v);
 #pragma unroll
-        for (int i = 0; i < EPV; ++i) n += X.y(Elem<T>::get(v, i)) >= lo_y ? 1 : 0;
+        for (int i = 0; i < EPV; ++i) n += Elem<T>::get(v, i) >= xlo ? 1 : 0;
       }
     const int incl_n = wave_incl_scan_i(n, lane);
     const int wtot = __builtin_amdgcn_readlane(incl_n, 63);
@@ -1234,7 +1286,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
 #pragma unroll
           for (int i = 0; i < EPV; ++i) {
             const float x = Elem<T>::get(v, i);
-            if (X.y(x) >= lo_y) {
+            if (x >= xlo) {
               const uint32_t kx = okey(x);
               if (pos < Smem<NT>::kWin)
                 S.wkey[pos] = ((uint64_t)kx << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
@@ -1261,12 +1313,17 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     const bool in = lane < nw && (uint32_t)(key >> 32) >= tkey;
     const uint32_t idx = 0xffffffffu - (uint32_t)(key & 0xffffffffu);
     const float ek = in ? e : 0.0f;
-    const uint64_t inb = __ballot(in);
+    S.we[lane] = ek;
+    S.widx[lane] = idx;
     double pre = 0.0;  // mass of kept elements with index <= mine
-    for (uint64_t m = inb; m; m &= m - 1) {
-      const int q = __ffsll((unsigned long long)m) - 1;
-      const uint32_t iq = (uint32_t)__builtin_amdgcn_readlane((int)idx, q);
-      if (iq <= idx) pre += (double)readlane_f(ek, q);
+    for (int q0 = 0; q0 < nw; q0 += 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int q = q0 + i;
+        const uint32_t iq = S.widx[q];
+        const float eq = S.we[q];
+        pre += (q < nw && iq <= idx) ? (double)eq : 0.0;
+      }
     }
     const int last = wave_max_i(in ? (int)idx : -1);
     const double total = readlane_d(pre, __ffsll((unsigned long long)__ballot(in && (int)idx == last)) - 1);
@@ -1316,7 +1373,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
 // One workgroup per output row b (grid = B_out).  WPE waves per SIMD: 8 lets two
 // 1024-thread workgroups share a CU, so one streams its row while the other
 // computes.
-template <bool GREEDY, typename T, int NT, int CAP, bool VEC, bool FULL, int WPE>
+template <bool GREEDY, typename T, int NT, int CAP, bool VEC, int FULL, int WPE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void sampler_kernel(SampleParams P) {
   __shared__ Smem<NT> S;
@@ -1346,6 +1403,7 @@ void sampler_kernel(SampleParams P) {
 // (n_rows_dev) exit at once.
 //   chunks per row NV <= 256*8    256 threads, 8 chunks each in registers
 //   NV <= 1024*8                  1024 threads, 8 chunks each (two per CU)
+//   NV <= 1024*16                 1024 threads, 16 chunks each (one per CU)
 //   longer rows                   1024 threads, 16 chunks each, the rest streamed
 // Unaligned rows (row start or stride not 16-byte aligned) use element loads.
 // ---------------------------------------------------------------------------
@@ -1358,11 +1416,13 @@ template <typename T, bool G>
 static void launch_rows(const SampleParams& P, bool vec, hipStream_t st) {
   constexpr int EPV = Elem<T>::EPV;
   const int64_t NV = (P.V + EPV - 1) / EPV;
-  if (!vec) launch(sampler_kernel<G, T, 1024, 16, false, false, 4>, 1024, P, st);
-  else if (NV <= 256 * 8) launch(sampler_kernel<G, T, 256, 8, true, false, 8>, 256, P, st);
-  else if (NV == 1024 * 8 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 8, true, true, 8>, 1024, P, st);
-  else if (NV <= 1024 * 8) launch(sampler_kernel<G, T, 1024, 8, true, false, 8>, 1024, P, st);
-  else launch(sampler_kernel<G, T, 1024, 16, true, false, 4>, 1024, P, st);
+  if (!vec) launch(sampler_kernel<G, T, 1024, 16, false, kStream, 4>, 1024, P, st);
+  else if (NV <= 256 * 8) launch(sampler_kernel<G, T, 256, 8, true, kBounded, 8>, 256, P, st);
+  else if (NV == 1024 * 8 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 8, true, kFull, 8>, 1024, P, st);
+  else if (NV <= 1024 * 8) launch(sampler_kernel<G, T, 1024, 8, true, kBounded, 8>, 1024, P, st);
+  else if (NV == 1024 * 16 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 16, true, kFull, 4>, 1024, P, st);
+  else if (NV <= 1024 * 16) launch(sampler_kernel<G, T, 1024, 16, true, kBounded, 4>, 1024, P, st);
+  else launch(sampler_kernel<G, T, 1024, 16, true, kStream, 4>, 1024, P, st);
 }
 
 template <typename T>
