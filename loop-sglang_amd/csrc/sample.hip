@@ -293,8 +293,19 @@ struct Smem {
   uint32_t kmin;           // smallest order key in the candidate window
   float we[kWave];         // small window: masses
   uint32_t widx[kWave];    // small window: vocabulary indices
-  uint64_t wkey[kWin];    // candidate window (unsorted)
-  uint64_t sorted[kWin];  // candidate window in descending key order
+  static constexpr int kSeg = kWave;     // candidates staged per wave
+  union {
+    uint64_t stage[NW * kSeg];  // per-wave candidate segments, in index order
+    struct {
+      uint64_t wkey[kWin];    // candidate window (unsorted)
+      uint64_t sorted[kWin];  // candidate window in descending key order
+    };
+  };
+  int wcnt[NW];            // candidates per wave
+  double rZ;               // row normaliser, histogram bin and candidate floor,
+  int rbin;                // derived by wave 0 for the whole workgroup
+  float rxlo;
+  uint64_t wwin[kWave];    // small window, in index order
   int wn;
   int pick;
 };
@@ -963,11 +974,12 @@ __device__ __forceinline__ float lds_max(const float* v) {
 // and its mass (e).  Each lane counts the entries at or above its own and sums
 // their masses, reading the window with broadcast LDS loads (keys are unique).
 template <int NT>
-__device__ __forceinline__ bool small_window(Smem<NT>& S, int nw, bool kon, int32_t k, bool pon, float p,
-                                             double Z, const Ex& X, uint32_t* tkey, uint64_t* key, float* e) {
+__device__ __forceinline__ bool small_window(Smem<NT>& S, const uint64_t* win, int nw, bool kon, int32_t k,
+                                             bool pon, float p, double Z, const Ex& X, uint32_t* tkey,
+                                             uint64_t* key, float* e) {
   const int lane = threadIdx.x & 63;
   const bool in = lane < nw;
-  const uint64_t mine = in ? S.wkey[lane] : 0ull;
+  const uint64_t mine = in ? win[lane] : 0ull;
   const uint32_t kx = (uint32_t)(mine >> 32);
   const float em = in ? X.e(okey_inv(kx)) : 0.0f;
   S.we[lane] = em;
@@ -977,7 +989,7 @@ __device__ __forceinline__ bool small_window(Smem<NT>& S, int nw, bool kon, int3
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int q = q0 + i;
-      const uint64_t other = S.wkey[q];
+      const uint64_t other = win[q];
       const float eo = S.we[q];
       const bool ge = q < nw && other >= mine;
       cnt += ge ? 1 : 0;
@@ -1194,16 +1206,19 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   double sw = 0.0;  // wave masses in the row's reference
   float fq = 0.0f;  // lane q < NW: wave q's mass factor and shift in bins
   int sq = kBins;
-  if (lane < NW) {
-    Ex Xq;
-    Xq.init(S.wmax[lane], c);
-    const float d = shift_diff(Xq, X);  // <= 0
-    fq = ex2c(d);
-    sw = S.wtot[lane] * (double)fq;
-    sq = d > -32.0f ? (int)__builtin_ceilf(-2.0f * d + 0x1p-10f) : kBins;
-  }
+  auto wave_refs = [&]() {
+    if (lane < NW) {
+      Ex Xq;
+      Xq.init(S.wmax[lane], c);
+      const float d = shift_diff(Xq, X);  // <= 0
+      fq = ex2c(d);
+      sw = S.wtot[lane] * (double)fq;
+      sq = d > -32.0f ? (int)__builtin_ceilf(-2.0f * d + 0x1p-10f) : kBins;
+    }
+  };
 
   if (!kon && !pon) {
+    wave_refs();
     int wstar;
     double base;
     const double U = cross_wave<NW>(sw, A.u, &wstar, &base);
@@ -1212,16 +1227,19 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     wave_walk<true>(R, cs, fw, base, U, [&](int) { return 0.0f; }, [&](float x) { return Xw.e(x); }, out);
     return;
   }
-  const double Z = wave_sum(sw);
 
   // ---- top-k / top-p: candidate window from the chunk maxima -------------
+  // Wave 0 derives the normaliser, the histogram bin and the candidate floor
+  // for the workgroup (done once, not by every wave: the waves would queue for
+  // the same SIMDs); the others wait at the barrier.
   // The count (top-k) or mass (top-p) of distinct elements at or above a bin
   // floor bounds that of all elements from below, so the first bin reaching k
   // or p*Z bounds the threshold from below.  Row bin r gathers bin r - s_q of
   // every wave q: a wave bin's contents sit at least s_q/2 lower in the row's
   // reference (s_q = ceil(2 * shift), with a margin for the rounding of y).
-  int bin;
-  {
+  if (wid == 0) {
+    wave_refs();
+    const double Zw = wave_sum(sw);
     int pc = 0;
     float pmf = 0.0f;
     int sqs[NW];
@@ -1246,14 +1264,22 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
     const int pcs = wave_incl_scan_i(pc, lane);
     const double pm = wave_incl_scan((double)pmf, lane);
-    const uint64_t bal = __ballot(kon ? (pcs >= A.k) : (pm >= (double)A.p * Z * kBinMargin));
-    bin = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
+    const uint64_t bal = __ballot(kon ? (pcs >= A.k) : (pm >= (double)A.p * Zw * kBinMargin));
+    const int b = bal ? (__ffsll((unsigned long long)bal) - 1) : -1;
+    const float xl = b >= 0 ? x_at_least(X, bin_floor(b)) : 0.0f;
+    if (lane == 0) {
+      S.rZ = Zw;
+      S.rbin = b;
+      S.rxlo = xl;
+    }
   }
+  __syncthreads();
+  const double Z = uni(S.rZ);
+  const int bin = uni(S.rbin);
   if (bin >= 0) {
     // Candidates: elements with y at or above the bin floor (x >= xlo), from
-    // the chunks whose maximum reaches it.  Count, reserve one range of the
-    // window per wave, write.
-    const float xlo = x_at_least(X, bin_floor(bin));  // candidate: x >= xlo
+    // the chunks whose maximum reaches it.
+    const float xlo = uni(S.rxlo);
     uint32_t km = 0;
     {
       typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
@@ -1262,83 +1288,105 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       for (int j = 0; j < CAP; ++j)
         if (R.has(j) && cmv.get(j) >= xlo) km |= 1u << j;
     }
-    int n = 0;
+    // Each wave writes its candidates into its own segment in index order
+    // (column j, then lane, then element): no atomics, and the window comes
+    // out sorted by vocabulary index.
+    uint64_t* seg = S.stage + wid * Smem<NT>::kSeg;
+    int run = 0;  // candidates of this wave so far (wave-uniform)
+    uint32_t kmn = 0xffffffffu;
 #pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      if (km & (1u << j)) {
+    for (int j = 0; j < CAP; ++j) {
+      const bool kj = (km >> j) & 1u;
+      if (__ballot(kj)) {
         uint4 v = R.d[j];
         launder(v);
+        int c = 0;
 #pragma unroll
-        for (int i = 0; i < EPV; ++i) n += Elem<T>::get(v, i) >= xlo ? 1 : 0;
-      }
-    const int incl_n = wave_incl_scan_i(n, lane);
-    const int wtot = __builtin_amdgcn_readlane(incl_n, 63);
-    if (wtot > 0) {
-      int base = 0;
-      if (lane == 63) base = atomicAdd(&S.wn, wtot);
-      int pos = __builtin_amdgcn_readlane(base, 63) + incl_n - n;
-      uint32_t kmn = 0xffffffffu;
+        for (int i = 0; i < EPV; ++i) c += kj && Elem<T>::get(v, i) >= xlo ? 1 : 0;
+        const int incl = wave_incl_scan_i(c, lane);
+        int pos = run + incl - c;
 #pragma unroll
-      for (int j = 0; j < CAP; ++j)
-        if (km & (1u << j)) {
-          uint4 v = R.d[j];
-          launder(v);
-#pragma unroll
-          for (int i = 0; i < EPV; ++i) {
-            const float x = Elem<T>::get(v, i);
-            if (x >= xlo) {
-              const uint32_t kx = okey(x);
-              if (pos < Smem<NT>::kWin)
-                S.wkey[pos] = ((uint64_t)kx << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
-              ++pos;
-              kmn = min(kmn, kx);
-            }
+        for (int i = 0; i < EPV; ++i) {
+          const float x = Elem<T>::get(v, i);
+          if (kj && x >= xlo) {
+            const uint32_t kx = okey(x);
+            if (pos < Smem<NT>::kSeg)
+              seg[pos] = ((uint64_t)kx << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
+            ++pos;
+            kmn = min(kmn, kx);
           }
         }
+        run += __builtin_amdgcn_readlane(incl, 63);
+      }
+    }
+    if (lane == 0) S.wcnt[wid] = run;
+    if (run > 0) {
       kmn = (uint32_t)wave_min_i((int)(kmn ^ 0x80000000u)) ^ 0x80000000u;
       if (lane == 0) atomicMin(&S.kmin, kmn);
     }
+  } else if (lane == 0) {
+    S.wcnt[wid] = 0;
   }
   __syncthreads();
-  const int nw = bin >= 0 ? uni(S.wn) : 0x7fffffff;
-  if (nw <= kWave) {
+  // window size, segment bases (lane q < NW) and overflow of a segment
+  const int cq = lane < NW ? S.wcnt[lane] : 0;
+  const int bq_incl = wave_incl_scan_i(cq, lane);
+  const int nw = bin >= 0 ? __builtin_amdgcn_readlane(bq_incl, NW - 1) : 0x7fffffff;
+  const bool ovf = __ballot(lane < NW && cq > Smem<NT>::kSeg) != 0;
+  if (nw <= kWave && !ovf) {
     // The window reaches the top-k count / top-p mass (bin test above), so
     // wave 0 finishes the row alone.
     if (wid != 0) return;
+    // gather entry `lane` of the window: segment w with base_w <= lane
+    int w = 0, bw = 0;
+#pragma unroll
+    for (int q = 1; q < NW; ++q) {
+      const int bq = __builtin_amdgcn_readlane(bq_incl - cq, q);
+      if (lane >= bq) {
+        w = q;
+        bw = bq;
+      }
+    }
+    const uint64_t ent = lane < nw ? S.stage[w * Smem<NT>::kSeg + (lane - bw)] : 0ull;
+    S.wwin[lane] = ent;
     uint32_t tkey;
     uint64_t key;
     float e;
-    if (!small_window<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &tkey, &key, &e)) tkey = 0u;  // unreachable
-    // walk the kept elements (key >= tkey) in ascending index order
+    if (!small_window<NT>(S, S.wwin, nw, kon, A.k, pon, A.p, Z, X, &tkey, &key, &e)) tkey = 0u;  // unreachable
+    // inverse CDF over the kept entries (key >= tkey); lanes are in index order
     const bool in = lane < nw && (uint32_t)(key >> 32) >= tkey;
-    const uint32_t idx = 0xffffffffu - (uint32_t)(key & 0xffffffffu);
+    const int32_t idx = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
     const float ek = in ? e : 0.0f;
-    S.we[lane] = ek;
-    S.widx[lane] = idx;
-    double pre = 0.0;  // mass of kept elements with index <= mine
-    for (int q0 = 0; q0 < nw; q0 += 8) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int q = q0 + i;
-        const uint32_t iq = S.widx[q];
-        const float eq = S.we[q];
-        pre += (q < nw && iq <= idx) ? (double)eq : 0.0;
-      }
-    }
-    const int last = wave_max_i(in ? (int)idx : -1);
-    const double total = readlane_d(pre, __ffsll((unsigned long long)__ballot(in && (int)idx == last)) - 1);
+    const double pre = wave_incl_scan((double)ek, lane);
+    const double total = readlane_d(pre, 63);
     float u = A.u;
     asm volatile("" : "+s"(u));
     const double U = (double)u * total;
-    const int pick = wave_min_i(in && ek > 0.0f && pre > U ? (int)idx : 0x7fffffff);
-    int id = pick;
-    if (pick == 0x7fffffff) id = wave_max_i(in && ek > 0.0f ? (int)idx : -1);
-    if (lane == 0) *out = id < 0 ? last : id;
+    const uint64_t cross = __ballot(ek > 0.0f && pre > U);
+    const uint64_t pos = __ballot(ek > 0.0f);
+    const uint64_t kept = __ballot(in);
+    int src;
+    if (cross) src = __ffsll((unsigned long long)cross) - 1;
+    else if (pos) src = 63 - __clzll((long long)pos);           // u >= 1 or rounding: last with mass
+    else src = kept ? 63 - __clzll((long long)kept) : 0;
+    const int id = __builtin_amdgcn_readlane(idx, src);
+    if (lane == 0) *out = id;
     return;
+  }
+  if (bin >= 0 && nw <= Smem<NT>::kWin && !ovf) {
+    // compact the segments into S.wkey[0, nw): read, barrier, write (the
+    // window overlaps the segments)
+    const int q = wid;
+    const int cw = __builtin_amdgcn_readlane(cq, q);
+    const int bw = __builtin_amdgcn_readlane(bq_incl - cq, q);
+    const uint64_t ent = lane < cw ? S.stage[q * Smem<NT>::kSeg + lane] : 0ull;
+    __syncthreads();
+    if (lane < cw) S.wkey[bw + lane] = ent;
+    __syncthreads();
   }
   // ---- larger windows: ranked by the workgroup (<= 512 candidates), else an
   // exact refinement over the window (or over the row when there is no bound)
-  if (bin >= 0 && nw <= Smem<NT>::kWin) {
+  if (bin >= 0 && nw <= Smem<NT>::kWin && !ovf) {
     float thr;
     if (window_threshold<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &thr)) {
       tmass = masked_masses(R, X, thr, cs);
