@@ -875,8 +875,10 @@ __device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, double t
 // This thread's chunk masses (register chunks) -> cs[j * NT] in LDS and its
 // total mass (chunks past CAP included).
 template <bool FMA, typename T, int NT, int CAP, bool VEC, int FULL>
-__device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float* cs) {
+__device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, float* cs,
+                                             float* cmass_max = nullptr) {
   double tmass = 0.0;
+  float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
     uint4 v = R.d[j];
@@ -884,7 +886,9 @@ __device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, cons
     const float sj = R.has(j) ? esum_chunk<T, FMA>(v, X) : 0.0f;
     cs[j * NT] = sj;
     tmass += (double)sj;
+    mx = fmaxf(mx, sj);
   }
+  if (cmass_max) *cmass_max = mx;  // largest register chunk mass
   for (int j = CAP; j < R.nstream(); ++j) tmass += (double)esum_chunk<T, FMA>(R.load(j), X);
   return tmass;
 }
@@ -1159,7 +1163,8 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   Ex Xw;  // this wave's shift
   Xw.init_u(wm, c);
   double tmass = 0.0;
-  if (tvalid) tmass = Xw.fma ? row_masses<true>(R, Xw, cs) : row_masses<false>(R, Xw, cs);
+  float cmx = 0.0f;  // largest chunk mass of this thread
+  if (tvalid) tmass = Xw.fma ? row_masses<true>(R, Xw, cs, &cmx) : row_masses<false>(R, Xw, cs, &cmx);
   {
     const double ws = wave_sum(tmass);
     if (lane == 0) {
@@ -1189,6 +1194,17 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     if (y2 >= kYMin) {
       if (kon) atomicAdd(&h[ybin(y2)], 1u);
       else atomicAdd(reinterpret_cast<float*>(&h[ybin(y2)]), ex2c(y2));
+    }
+    if (!kon && y1 >= kYMin) {
+      // The chunk of largest mass M (n = EPV elements, thread maximum m): at
+      // any level L at or below y_e = log2((M - m) / (2 (n - 1))) its elements
+      // at or above L weigh at least M - (n - 1) 2^L >= (M + m) / 2, which
+      // covers what the two maxima above counted from it plus (M - m) / 2.
+      // Adds (M - m) / 2 at y_e, so rows whose heaviest elements share a chunk
+      // still get a bound.
+      const float rest = cmx - ex2c(y1);
+      const float ye = rest > 0.0f ? __log2f(rest * (0.5f / (float)(EPV - 1))) : -INFINITY;
+      if (ye >= kYMin) atomicAdd(reinterpret_cast<float*>(&h[ybin(ye)]), 0.5f * rest);
     }
   }
   __syncthreads();
