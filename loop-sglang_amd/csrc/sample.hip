@@ -325,6 +325,7 @@ struct Row {
   using CM = ChunkMax<T, CAP>;
   static constexpr int kCmWords = sizeof(CM) / 4;
   const char* base;
+  __amdgpu_buffer_rsrc_t rsrc;
   uint32_t V;
   int L;
   uint32_t c0;  // chunk index of this thread's j = 0 load
@@ -334,6 +335,9 @@ struct Row {
   __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, int64_t Vv, uint32_t* cm_lds) {
     cmx = cm_lds + threadIdx.x * kCmWords;
     base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)Elem<T>::kSize;
+    // Buffer resource over the row: full chunks load with one 32-bit lane
+    // offset plus a scalar offset per j (one address register for every load).
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)0xffffffff, 0x00020000);
     V = (uint32_t)uni((uint32_t)Vv);
     const uint32_t NV = (V + EPV - 1) / EPV;
     L = FULL == kFull ? CAP : (int)((NV + NT - 1) / NT);
@@ -346,7 +350,11 @@ struct Row {
   }
   __device__ __forceinline__ uint32_t chunk_index(int j) const { return c0 + (uint32_t)j * kWave; }
   __device__ __forceinline__ uint4 load(int j) const {
-    if (FULL == kFull) return *reinterpret_cast<const uint4*>(base + chunk_index(j) * 16u);
+    if (FULL == kFull || (VEC && (chunk_index(j) + 1u) * EPV <= V)) {
+      typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+      const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)(c0 * 16u), j * kWave * 16, 0);
+      return make_uint4(v.x, v.y, v.z, v.w);
+    }
     return load_chunk32<T, VEC>(base, chunk_index(j), V);
   }
   __device__ __forceinline__ uint32_t elem_index(int j, int i) const {
