@@ -43,6 +43,9 @@ struct Elem<float> {
     const uint32_t w = i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
     return __uint_as_float(w);
   }
+  // (no unpacking: a second pass shares nothing with the first)
+  __device__ static __forceinline__ float get_alt(const uint4& v, int i) { return get(v, i); }
+  static constexpr bool kHasAlt = true;
   __device__ static __forceinline__ uint4 pad() {
     return make_uint4(0xff800000u, 0xff800000u, 0xff800000u, 0xff800000u);
   }
@@ -63,6 +66,15 @@ struct Elem<bf16_t> {
     const uint32_t w = k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
     return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
   }
+  // Same value through a byte permute: a second pass over the same registers
+  // unpacks with different instructions, so the compiler cannot keep the first
+  // pass's unpacked values alive for it (that would double the registers).
+  __device__ static __forceinline__ float get_alt(const uint4& v, int i) {
+    const int k = i >> 1;
+    const uint32_t w = k == 0 ? v.x : (k == 1 ? v.y : (k == 2 ? v.z : v.w));
+    return __uint_as_float(__builtin_amdgcn_perm(0u, w, (i & 1) ? 0x03020c0cu : 0x01000c0cu));
+  }
+  static constexpr bool kHasAlt = true;
   __device__ static __forceinline__ uint4 pad() {
     return make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);
   }
@@ -84,6 +96,9 @@ struct Elem<f16_t> {
     const uint16_t h = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
     return (float)__builtin_bit_cast(_Float16, h);
   }
+  // (same conversions: a second pass launders the registers instead)
+  __device__ static __forceinline__ float get_alt(const uint4& v, int i) { return get(v, i); }
+  static constexpr bool kHasAlt = false;
   __device__ static __forceinline__ uint4 pad() {
     return make_uint4(0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u);
   }

@@ -149,7 +149,7 @@ __device__ __forceinline__ float esum_chunk(const uint4& v, const Ex& X) {
   float e[EPV];
 #pragma unroll
   for (int i = 0; i < EPV; ++i) {
-    const float x = Elem<T>::get(v, i);
+    const float x = Elem<T>::get_alt(v, i);
     e[i] = ex2c(FMA ? __builtin_fmaf(x, X.c, X.nb) : (x - X.gm) * X.c);
   }
   return tree_sum<EPV>(e);
@@ -890,7 +890,7 @@ __device__ __forceinline__ double row_masses(Row<T, NT, CAP, VEC, FULL>& R, cons
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
     uint4 v = R.d[j];
-    launder(v);  // no unpacked value is shared with the maxima pass
+    if constexpr (!Elem<T>::kHasAlt) launder(v);  // no unpacked value is shared with the maxima pass
     const float sj = R.has(j) ? esum_chunk<T, FMA>(v, X) : 0.0f;
     cs[j * NT] = sj;
     tmass += (double)sj;
