@@ -38,6 +38,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 // exactly NT*CAP full chunks.
 constexpr int kStream = 0, kBounded = 2, kFull = 1;
 constexpr int kBins = 64;  // histogram of y = log2(e / e_max): bins of width 1/2
+constexpr int kRefBins = 256;             // exact refinement: bins per level
+constexpr double kFix = 1099511627776.0;  // exact refinement: mass fixed point, 2^40
 constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
 // Margin on the top-p histogram test: the bin is chosen where the float sum of
 // the binned maxima reaches p*Z*(1 + 2^-10), so the window (a superset of those
@@ -288,9 +290,8 @@ struct Smem {
   int hcnt[kBins];
   float hmass[kBins];
   uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass as float bits)
-  int fcnt[kBins];         // refinement bins: member count
-  double fmass[kBins];     // refinement bins: member mass
   uint32_t kmin;           // smallest order key in the candidate window
+  unsigned long long rbins[4][kRefBins];  // exact refinement: bin copies by lane
   float we[kWave];         // small window: masses
   uint32_t widx[kWave];    // small window: vocabulary indices
   static constexpr int kSeg = kWave;     // candidates staged per wave
@@ -1033,63 +1034,73 @@ __device__ __forceinline__ bool small_window(Smem<NT>& S, const uint64_t* win, i
 // Exact top-k (count target k) or top-p (mass target p * ZK) threshold by radix
 // refinement in order-key space (key = okey(x) >> SH).  Members are the non-NaN
 // elements with key >= klo; the boundary lies among them.  Each level splits
-// the bracket [lo, hi) of keys that holds the boundary into 64 bins of 2^sh
-// keys, counts the members per bin (and sums their masses in double), and
-// scans from the top with the totals above the bracket to pick the bin that
-// holds the boundary.  A bin of one key is the answer (ties are kept); a bin
-// of at most 64 members is ranked by wave 0.  Returns false when the members
-// never reach the target.  All waves of the workgroup call it together.
+// the bracket [lo, hi) of keys that holds the boundary into 256 bins of 2^sh
+// keys and accumulates per bin the member count (top-k) or mass (top-p, fixed
+// point with 40 fraction bits: exact, order-independent sums) with one LDS
+// atomic per member, into four copies of the bins picked by lane (fewer lanes
+// on one address).  A scan from the top with the totals above the bracket
+// picks the bin holding the boundary; the next level splits that bin, down to
+// a single key (the answer; ties are kept): two levels for bf16 keys, three
+// for fp16, four for fp32.  Returns false when the members never reach the
+// target.  All waves of the workgroup call it together.
 // ---------------------------------------------------------------------------
 template <int NT, typename T, class R_>
 __device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, bool kon, int32_t k, float p,
                                                  uint32_t klo, Smem<NT>& S, uint32_t* thr_key) {
   constexpr int SH = KeyShift<T>::value, EPV = Elem<T>::EPV;
-  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
   uint32_t lo = klo, hi = (okey(X.gm) >> SH) + 1u;  // keys in [lo, hi)
-  int above_c = 0;
-  double above_m = 0.0;
-  const double target = (double)p * ZK;
-  for (;;) {
+  double above = 0.0;  // count or fixed-point mass of the members above hi
+  const double target = kon ? (double)k : (double)p * ZK * kFix;
+  unsigned long long* bins = S.rbins[0];
+  for (int level = 0; level < 8; ++level) {
     if (hi <= lo) return false;
     int sh = 0;
-    while (((hi - lo - 1u) >> sh) >= (uint32_t)kBins) ++sh;
-    if (t < kBins) {
-      S.fcnt[t] = 0;
-      S.fmass[t] = 0.0;
-    }
-    if (t == 0) S.wn = 0;
+    while (((hi - lo - 1u) >> sh) >= (uint32_t)kRefBins) ++sh;
+    for (int i = t; i < 4 * kRefBins; i += NT) bins[i] = 0ull;
     __syncthreads();
     const uint32_t lo_ = lo, hi_ = hi;
-    auto member = [&](float x, uint32_t* key) {
-      *key = okey(x) >> SH;
-      return x == x && *key >= lo_ && *key < hi_;
-    };
     const float xlo = okey_inv(lo << SH);  // smallest value with key lo (NaN for lo == 0)
-    auto keep = [&](float m) { return lo == 0u || m >= xlo; };
-    R.each_kept_mem(keep,
+    unsigned long long* mine = S.rbins[lane & 3];
+    R.each_kept_mem([&](float m) { return lo_ == 0u || m >= xlo; },
                     [&](int, const uint4& v, float) {
-#pragma unroll 1
+#pragma unroll
                       for (int i = 0; i < EPV; ++i) {
                         const float x = Elem<T>::get(v, i);
-                        uint32_t key;
-                        if (member(x, &key)) {
+                        const uint32_t key = okey(x) >> SH;
+                        if (x == x && key >= lo_ && key < hi_) {
                           const int b = (int)((hi_ - 1u - key) >> sh);
-                          atomicAdd(&S.fcnt[b], 1);
-                          if (!kon) atomicAdd(&S.fmass[b], (double)X.e(x));
+                          const unsigned long long add =
+                              kon ? 1ull : (unsigned long long)((double)X.e(x) * kFix + 0.5);
+                          atomicAdd(&mine[b], add);
                         }
                       }
                     });
     __syncthreads();
-    const int cb = S.fcnt[lane];
-    const double mb = kon ? 0.0 : S.fmass[lane];
-    const int ic = wave_incl_scan_i(cb, lane);
-    const double im = wave_incl_scan(mb, lane);
-    const uint64_t bal = __ballot(kon ? (above_c + ic >= k) : (above_m + im >= target));
+    // lane l holds bins 4l .. 4l+3 (summed over the four copies), every wave
+    double bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int bi = 4 * lane + q;
+      bv[q] = (double)(S.rbins[0][bi] + S.rbins[1][bi] + S.rbins[2][bi] + S.rbins[3][bi]);
+    }
+    const double ls = (bv[0] + bv[1]) + (bv[2] + bv[3]);
+    const double incl = wave_incl_scan(ls, lane);
+    const uint64_t bal = __ballot(above + incl >= target);
     if (!bal) return false;
-    const int bs = __ffsll((unsigned long long)bal) - 1;
-    const int cnt = __builtin_amdgcn_readlane(cb, bs);
-    above_c += __builtin_amdgcn_readlane(ic - cb, bs);
-    above_m += readlane_d(im - mb, bs);
+    const int lb = __ffsll((unsigned long long)bal) - 1;
+    double acc = above + readlane_d(incl - ls, lb);  // members above lane lb's bins
+    int bs = 4 * lb + 3;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const double vq = readlane_d(bv[q], lb);
+      if (acc + vq >= target) {
+        bs = 4 * lb + q;
+        break;
+      }
+      acc += vq;
+    }
+    above = acc;  // members above bin bs
     const uint32_t nhi = hi - ((uint32_t)bs << sh);
     const uint32_t nlo = nhi - lo > (1u << sh) ? nhi - (1u << sh) : lo;
     __syncthreads();  // every wave has read the bins
@@ -1099,48 +1110,8 @@ __device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, 
       *thr_key = lo;
       return true;
     }
-    if (cnt > kWave) continue;
-    // Final: rank the boundary bin's members (at most 64) in wave 0.
-    const float xlo2 = okey_inv(lo << SH);
-    R.each_kept_mem([&](float m) { return lo == 0u || m >= xlo2; },
-                    [&](int j, const uint4& v, float) {
-#pragma unroll 1
-                      for (int i = 0; i < EPV; ++i) {
-                        const float x = Elem<T>::get(v, i);
-                        const uint32_t key = okey(x) >> SH;
-                        if (x == x && key >= lo && key < hi) {
-                          const int pos = atomicAdd(&S.wn, 1);
-                          if (pos < kWave)
-                            S.wkey[pos] = ((uint64_t)okey(x) << 32) | (uint64_t)(0xffffffffu - R.elem_index(j, i));
-                        }
-                      }
-                    });
-    __syncthreads();
-    if (wid == 0) {
-      const int n = min(uni(S.wn), kWave);
-      const uint64_t mine = lane < n ? S.wkey[lane] : 0ull;
-      const float e = (lane < n && !kon) ? X.e(okey_inv((uint32_t)(mine >> 32))) : 0.0f;
-      int rank = 0;      // members above mine
-      double pre = 0.0;  // mass of members at or above mine (keys are unique)
-      for (int q = 0; q < n; ++q) {
-        const uint64_t other = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), q) << 32) |
-                               (uint32_t)__builtin_amdgcn_readlane((int)(mine & 0xffffffffu), q);
-        rank += other > mine ? 1 : 0;
-        if (other >= mine) pre += (double)readlane_f(e, q);
-      }
-      const bool hit = lane < n && (kon ? (above_c + rank + 1 >= k) : (above_m + pre >= target));
-      // the hit with the smallest rank is the boundary element
-      const int r = wave_min_i(hit ? rank : 0x7fffffff);
-      const uint64_t who = __ballot(hit && rank == r);
-      if (lane == 0) S.pick = who ? (int)(__builtin_amdgcn_readlane((int)(mine >> 32), __ffsll((unsigned long long)who) - 1)) : 0;
-      if (lane == 0) S.wn = who ? 1 : 0;
-    }
-    __syncthreads();
-    const bool found = uni(S.wn) != 0;
-    *thr_key = (uint32_t)uni(S.pick) >> SH;
-    __syncthreads();
-    return found;
   }
+  return false;
 }
 
 template <typename T, int NT, int CAP, bool VEC, int FULL>
@@ -1420,7 +1391,11 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
   }
   constexpr int SH = KeyShift<T>::value;
-  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH) : 0u;
+  // Members: the candidate window, or (no bound) every element with mass at
+  // least 2^-40 of the maximum: below that, the whole rest of the row weighs
+  // less than 2^-24 of Z, so a boundary there is within the parity tolerance
+  // whichever way it falls.
+  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH);
   uint32_t tk = 0;
   bool ok;
   if (kon) {
