@@ -291,7 +291,7 @@ struct Smem {
   float hmass[kBins];
   uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass as float bits)
   uint32_t kmin;           // smallest order key in the candidate window
-  unsigned long long rbins[4][kRefBins];  // exact refinement: bin copies by lane
+  unsigned long long rbins[4][kRefBins + 1];  // exact refinement: bin copies by lane, one bin apart in bank order
   float we[kWave];         // small window: masses
   uint32_t widx[kWave];    // small window: vocabulary indices
   static constexpr int kSeg = kWave;     // candidates staged per wave
@@ -1057,7 +1057,7 @@ __device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, 
     if (hi <= lo) return false;
     int sh = 0;
     while (((hi - lo - 1u) >> sh) >= (uint32_t)kRefBins) ++sh;
-    for (int i = t; i < 4 * kRefBins; i += NT) bins[i] = 0ull;
+    for (int i = t; i < 4 * (kRefBins + 1); i += NT) bins[i] = 0ull;
     __syncthreads();
     const uint32_t lo_ = lo, hi_ = hi;
     const float xlo = okey_inv(lo << SH);  // smallest value with key lo (NaN for lo == 0)

@@ -256,8 +256,9 @@ def test_sampler_prepare_and_sample(lsg, orc, dev):
     s = lsg.Sampler(dev, 3000)
     args = s.prepare(SimpleNamespace(reqs=reqs))
     assert args.temperatures is not None
-    x = torch.randn(4, 3000, device=dev)
-    args.uniforms = torch.rand(4, device=dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(4, 3000, device=dev, generator=g)
+    args.uniforms = torch.rand(4, device=dev, generator=g)
     ids = s.sample(x, args)
     check_sampling(lsg, orc, x, args.temperatures, args.top_k, args.top_p, args.uniforms)
     # rows 0 and 3 are greedy: T = 1e-6 puts all mass on the argmax
