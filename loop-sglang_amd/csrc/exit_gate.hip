@@ -145,13 +145,22 @@ __device__ void compact_rows(const GateParams& P) {
   }
 }
 
-// Arrival counting; the last workgroup compacts.  Every row leader has already
-// published its bit with an agent-scope fence.
-__device__ __forceinline__ void finish_block(const GateParams& P) {
+// Publication and arrival counting, once per workgroup: the row leaders set
+// their exit bits in LDS (bits [0, RPB) of s_bits, rows row0 .. row0+RPB-1 in
+// one 32-bit word since RPB divides 32); thread 0 ORs them into the workspace
+// bitmask, fences (orders the bits before its arrival) and counts the arrival.
+// The last workgroup to arrive compacts.  No other cross-workgroup data: the
+// per-row outputs are read by later kernels only.
+template <int RPB>
+__device__ __forceinline__ void finish_block(const GateParams& P, const uint32_t* s_bits) {
   if (!P.counter) return;
+  static_assert(32 % RPB == 0, "a workgroup's rows share one bitmask word");
   __shared__ int s_last;
   __syncthreads();
   if (threadIdx.x == 0) {
+    const int64_t row0 = (int64_t)blockIdx.x * RPB;
+    const uint32_t b = *s_bits;
+    if (b) atomicOr(&P.bits[row0 >> 5], b << (row0 & 31));
     __threadfence();
     const uint32_t prev = atomicAdd(P.counter, 1u);
     s_last = prev == gridDim.x - 1;
@@ -163,10 +172,33 @@ __device__ __forceinline__ void finish_block(const GateParams& P) {
   }
 }
 
-__device__ __forceinline__ void publish_bit(const GateParams& P, int64_t row, int m) {
-  if (P.bits && m) {
-    atomicOr(&P.bits[row >> 5], 1u << (row & 31));
-    __threadfence();
+// f(a_i, b_i) over this thread's elements of two rows: chunks c = tr,
+// tr + TPR, ... in order, elements in order (the sequence of a plain loop).
+// Full 16-byte chunks load four pairs at a time, so their loads are in flight
+// together; the partial last chunk is bounds-checked.
+template <typename T, int TPR, bool VEC, class F>
+__device__ __forceinline__ void row_pairs(const T* a, const T* b, int64_t H, int tr, F&& f) {
+  constexpr int EPV = Elem<T>::EPV, U = 4;
+  const int64_t nfull = VEC ? H / EPV : 0;
+  int64_t c = tr;
+  for (; c + (U - 1) * TPR < nfull; c += U * TPR) {
+    uint4 av[U], bv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      av[u] = *reinterpret_cast<const uint4*>(a + (c + u * TPR) * EPV);
+      bv[u] = *reinterpret_cast<const uint4*>(b + (c + u * TPR) * EPV);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) f(Elem<T>::get(av[u], i), Elem<T>::get(bv[u], i));
+  }
+  const int64_t nch = (H + EPV - 1) / EPV;
+  for (; c < nch; c += TPR) {
+    const uint4 av = load_chunk<T, VEC>(a, c, H), bv = load_chunk<T, VEC>(b, c, H);
+#pragma unroll
+    for (int i = 0; i < EPV; ++i)
+      if (c * EPV + i < H) f(Elem<T>::get(av, i), Elem<T>::get(bv, i));
   }
 }
 
@@ -174,6 +206,9 @@ template <typename T, int TPR, bool VEC>
 __global__ __launch_bounds__(kGateThreads) void ouro_gate_kernel(GateParams P) {
   constexpr int EPV = Elem<T>::EPV, RPB = kGateThreads / TPR;
   __shared__ float s_part[kGateThreads / kWave];
+  __shared__ uint32_t s_bits;
+  if (threadIdx.x == 0) s_bits = 0u;
+  __syncthreads();  // cleared before any row leader sets its bit
   const int tr = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
   const int64_t nch = (P.H + EPV - 1) / EPV;
@@ -181,13 +216,7 @@ __global__ __launch_bounds__(kGateThreads) void ouro_gate_kernel(GateParams P) {
   if (row < P.B) {
     const T* hrow = reinterpret_cast<const T*>(P.h) + row * P.ldh;
     const T* wrow = reinterpret_cast<const T*>(P.w);
-    for (int64_t c = tr; c < nch; c += TPR) {
-      const uint4 hv = load_chunk<T, VEC>(hrow, c, P.H);
-      const uint4 wv = load_chunk<T, VEC>(wrow, c, P.H);
-#pragma unroll
-      for (int i = 0; i < EPV; ++i)
-        if (c * EPV + i < P.H) acc = fmaf(Elem<T>::get(hv, i), Elem<T>::get(wv, i), acc);
-    }
+    row_pairs<T, TPR, VEC>(hrow, wrow, P.H, tr, [&](float x, float y) { acc = fmaf(x, y, acc); });
   }
   acc = row_sum<TPR>(acc, s_part);
   if (row < P.B && tr == 0) {
@@ -202,15 +231,18 @@ __global__ __launch_bounds__(kGateThreads) void ouro_gate_kernel(GateParams P) {
     P.F_next[s] = Fn;
     P.mask[row] = (uint8_t)m;
     if (P.aux_out) P.aux_out[row] = z;
-    publish_bit(P, row, m);
+    if (m) atomicOr(&s_bits, 1u << (threadIdx.x / TPR));
   }
-  finish_block(P);
+  finish_block<RPB>(P, &s_bits);
 }
 
 template <typename T, int TPR, bool VEC>
 __global__ __launch_bounds__(kGateThreads) void rel_change_kernel(GateParams P) {
   constexpr int EPV = Elem<T>::EPV, RPB = kGateThreads / TPR;
   __shared__ float s_part[kGateThreads / kWave];
+  __shared__ uint32_t s_bits;
+  if (threadIdx.x == 0) s_bits = 0u;
+  __syncthreads();  // cleared before any row leader sets its bit
   const int tr = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
   const int64_t nch = (P.H + EPV - 1) / EPV;
@@ -218,19 +250,11 @@ __global__ __launch_bounds__(kGateThreads) void rel_change_kernel(GateParams P) 
   if (row < P.B) {
     const T* a = reinterpret_cast<const T*>(P.h) + row * P.ldh;
     const T* bp = reinterpret_cast<const T*>(P.hp) + row * P.ldp;
-    for (int64_t c = tr; c < nch; c += TPR) {
-      const uint4 av = load_chunk<T, VEC>(a, c, P.H);
-      const uint4 bv = load_chunk<T, VEC>(bp, c, P.H);
-#pragma unroll
-      for (int i = 0; i < EPV; ++i) {
-        if (c * EPV + i < P.H) {
-          const float x = Elem<T>::get(av, i), y = Elem<T>::get(bv, i);
-          const float dd = x - y;
-          d2 = fmaf(dd, dd, d2);
-          n2 = fmaf(x, x, n2);
-        }
-      }
-    }
+    row_pairs<T, TPR, VEC>(a, bp, P.H, tr, [&](float x, float y) {
+      const float dd = x - y;
+      d2 = fmaf(dd, dd, d2);
+      n2 = fmaf(x, x, n2);
+    });
   }
   d2 = row_sum<TPR>(d2, s_part);
   n2 = row_sum<TPR>(n2, s_part);
@@ -239,9 +263,9 @@ __global__ __launch_bounds__(kGateThreads) void rel_change_kernel(GateParams P) 
     const int m = ratio < P.tau;
     P.mask[row] = (uint8_t)m;
     if (P.aux_out) P.aux_out[row] = ratio;
-    publish_bit(P, row, m);
+    if (m) atomicOr(&s_bits, 1u << (threadIdx.x / TPR));
   }
-  finish_block(P);
+  finish_block<RPB>(P, &s_bits);
 }
 
 template <typename T>
@@ -264,10 +288,11 @@ template <typename T>
 static void launch_rows(GateKind kind, const GateParams& P, bool vec, hipStream_t st) {
   constexpr int EPV = Elem<T>::EPV;
   const int64_t nch = (P.H + EPV - 1) / EPV;
-  // threads per row: enough 16-byte chunks per thread to keep loads in flight
-  if (nch <= 64) vec ? launch_kind<T, 64, true>(kind, P, st) : launch_kind<T, 64, false>(kind, P, st);
-  else if (nch <= 128) vec ? launch_kind<T, 128, true>(kind, P, st) : launch_kind<T, 128, false>(kind, P, st);
-  else vec ? launch_kind<T, 256, true>(kind, P, st) : launch_kind<T, 256, false>(kind, P, st);
+  // one wave per row, four rows per workgroup: a row's loads are issued
+  // back to back (nch / 64 chunks per thread), and publication costs one
+  // fence and one counter atomic per four rows
+  (void)nch;
+  vec ? launch_kind<T, kWave, true>(kind, P, st) : launch_kind<T, kWave, false>(kind, P, st);
 }
 
 static int dispatch_rows(GateKind kind, int dtype, const GateParams& P, bool vec, hipStream_t st) {
