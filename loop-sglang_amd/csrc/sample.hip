@@ -1391,11 +1391,13 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
   }
   constexpr int SH = KeyShift<T>::value;
-  // Members: the candidate window, or (no bound) every element with mass at
-  // least 2^-40 of the maximum: below that, the whole rest of the row weighs
-  // less than 2^-24 of Z, so a boundary there is within the parity tolerance
-  // whichever way it falls.
-  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH);
+  // Members: the candidate window, or (no bound) for top-k every non-NaN
+  // element (the k-th largest can sit any distance below the maximum), for
+  // top-p every element with mass at least 2^-40 of the maximum: below that,
+  // the whole rest of the row weighs less than 2^-24 of Z, so a boundary there
+  // is within the parity tolerance whichever way it falls.
+  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
+                                : (kon ? (okey(-INFINITY) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH));
   uint32_t tk = 0;
   bool ok;
   if (kon) {
