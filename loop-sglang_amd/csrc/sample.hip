@@ -1114,6 +1114,64 @@ __device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, 
   return false;
 }
 
+// Floor for the k-th largest element from the threads' maxima (k <= NT): the
+// k largest thread maxima are distinct elements, so at least k elements are at
+// or above the k-th largest.  One radix level over the thread maxima's order
+// keys in [lo, hi) (256 bins, counts; one LDS atomic per thread) returns the
+// floor key of the bin holding it, or lo when k > NT or fewer than k threads
+// have a maximum in range.  Reads only the chunk maxima (LDS); all waves call
+// it together.
+template <int NT, typename T, class R_>
+__device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t lo, uint32_t hi, Smem<NT>& S) {
+  constexpr int SH = KeyShift<T>::value;
+  const int t = threadIdx.x, lane = t & 63;
+  if (hi <= lo + 1u) return lo;
+  int sh = 0;
+  while (((hi - lo - 1u) >> sh) >= (uint32_t)kRefBins) ++sh;
+  unsigned long long* bins = S.rbins[0];
+  for (int i = t; i < 4 * (kRefBins + 1); i += NT) bins[i] = 0ull;
+  __syncthreads();
+  unsigned long long* mine = S.rbins[lane & 3];
+  float tmax = -INFINITY;
+  bool any = false;
+  R.each_cm([&](int, float m) {
+    if (m == m) {
+      tmax = fmaxf(tmax, m);
+      any = true;
+    }
+  });
+  const uint32_t key = okey(tmax) >> SH;
+  if (any && k <= NT && key >= lo && key < hi) atomicAdd(&mine[(hi - 1u - key) >> sh], 1ull);
+  __syncthreads();
+  unsigned long long bv[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int bi = 4 * lane + q;
+    bv[q] = S.rbins[0][bi] + S.rbins[1][bi] + S.rbins[2][bi] + S.rbins[3][bi];
+  }
+  const double ls = (double)((bv[0] + bv[1]) + (bv[2] + bv[3]));
+  const double incl = wave_incl_scan(ls, lane);  // counts: exact in double
+  const uint64_t bal = __ballot(incl >= (double)k);
+  uint32_t fl = lo;
+  if (bal) {
+    const int lb = __ffsll((unsigned long long)bal) - 1;
+    double acc = readlane_d(incl - ls, lb);
+    int bs = 4 * lb + 3;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      acc += (double)__builtin_amdgcn_readlane((int)bv[q], lb);
+      if (acc >= (double)k) {
+        bs = 4 * lb + q;
+        break;
+      }
+    }
+    const uint32_t top = hi - ((uint32_t)bs << sh);  // bin bs holds keys [top - 2^sh, top)
+    fl = top - lo > (1u << sh) ? top - (1u << sh) : lo;
+  }
+  __syncthreads();  // every wave has read the bins
+  return fl;
+}
+
 template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
                                                  Smem<NT>& S, float* csum) {
@@ -1396,8 +1454,9 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   // top-p every element with mass at least 2^-40 of the maximum: below that,
   // the whole rest of the row weighs less than 2^-24 of Z, so a boundary there
   // is within the parity tolerance whichever way it falls.
-  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
-                                : (kon ? (okey(-INFINITY) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH));
+  uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
+                          : (kon ? (okey(-INFINITY) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH));
+  if (kon && bin < 0) klo = chunk_max_floor<NT, T>(R, A.k, klo, (okey(X.gm) >> SH) + 1u, S);
   uint32_t tk = 0;
   bool ok;
   if (kon) {
