@@ -1328,11 +1328,25 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   }
   __syncthreads();
   const double Z = uni(S.rZ);
-  const int bin = uni(S.rbin);
+  constexpr int SH = KeyShift<T>::value;
+  int bin = uni(S.rbin);
+  float xlo = 0.0f;
   if (bin >= 0) {
-    // Candidates: elements with y at or above the bin floor (x >= xlo), from
-    // the chunks whose maximum reaches it.
-    const float xlo = uni(S.rxlo);
+    xlo = uni(S.rxlo);
+  } else if (kon) {
+    // top-k beyond the histogram's reach (the k-th largest is more than 32
+    // binary orders of magnitude below the maximum): the floor from the
+    // threads' maxima bounds it instead
+    const uint32_t kneg = okey(-INFINITY) >> SH;
+    const uint32_t fl = chunk_max_floor<NT, T>(R, A.k, kneg, (okey(X.gm) >> SH) + 1u, S);
+    if (fl > kneg) {
+      bin = 0;
+      xlo = okey_inv(fl << SH);  // x >= xlo exactly when key >= fl
+    }
+  }
+  if (bin >= 0) {
+    // Candidates: elements at or above the floor (x >= xlo), from the chunks
+    // whose maximum reaches it.
     uint32_t km = 0;
     {
       typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
@@ -1448,15 +1462,13 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       return;
     }
   }
-  constexpr int SH = KeyShift<T>::value;
   // Members: the candidate window, or (no bound) for top-k every non-NaN
   // element (the k-th largest can sit any distance below the maximum), for
   // top-p every element with mass at least 2^-40 of the maximum: below that,
   // the whole rest of the row weighs less than 2^-24 of Z, so a boundary there
   // is within the parity tolerance whichever way it falls.
-  uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
-                          : (kon ? (okey(-INFINITY) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH));
-  if (kon && bin < 0) klo = chunk_max_floor<NT, T>(R, A.k, klo, (okey(X.gm) >> SH) + 1u, S);
+  const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
+                                : (kon ? (okey(-INFINITY) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH));
   uint32_t tk = 0;
   bool ok;
   if (kon) {
