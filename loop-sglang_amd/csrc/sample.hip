@@ -292,8 +292,7 @@ struct Smem {
   uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass as float bits)
   uint32_t kmin;           // smallest order key in the candidate window
   unsigned long long rbins[4][kRefBins + 1];  // exact refinement: bin copies by lane, one bin apart in bank order
-  float we[kWave];         // small window: masses
-  uint32_t widx[kWave];    // small window: vocabulary indices
+  float we[2 * kWave];     // small window: masses
   static constexpr int kSeg = kWave;     // candidates staged per wave
   union {
     uint64_t stage[NW * kSeg];  // per-wave candidate segments, in index order
@@ -306,7 +305,7 @@ struct Smem {
   double rZ;               // row normaliser, histogram bin and candidate floor,
   int rbin;                // derived by wave 0 for the whole workgroup
   float rxlo;
-  uint64_t wwin[kWave];    // small window, in index order
+  uint64_t wwin[2 * kWave];  // small window, in index order
   int wn;
   int pick;
 };
@@ -715,10 +714,24 @@ __device__ __forceinline__ RowArgs row_args(const SampleParams& P, int64_t r) {
   return a;
 }
 
+// The same arguments as plain loads, made wave-uniform by uniform() where the
+// row is processed.  They are vector loads: converting right after them waits
+// for them, so the kernel issues them, then the row's chunks, then converts
+// (the in-order counter then waits for the arguments only).
+__device__ __forceinline__ RowArgs row_args_load(const SampleParams& P, int64_t r) {
+  RowArgs a;
+  a.T = P.temps ? P.temps[r] : 0.0f;
+  a.u = P.uniforms ? P.uniforms[r] : 0.0f;
+  a.k = P.top_k ? P.top_k[r] : 0;
+  a.p = P.top_p ? P.top_p[r] : 1.0f;
+  return a;
+}
+__device__ __forceinline__ RowArgs uniform(const RowArgs& a) { return RowArgs{uni(a.T), uni(a.p), uni(a.u), uni(a.k)}; }
+
 // Output row b -> source row r: >= 0 valid, -1 past the end, -2 invalid gather index.
 __device__ __forceinline__ int64_t source_row(const SampleParams& P, int64_t b, int64_t nrows) {
   if (b >= nrows) return -1;
-  const int64_t r = P.row_idx ? (int64_t)P.row_idx[b] : b;
+  const int64_t r = P.row_idx ? (int64_t)uni((int)P.row_idx[b]) : b;
   return (r < 0 || r >= P.B_src) ? -2 : r;
 }
 
@@ -981,52 +994,76 @@ __device__ __forceinline__ float lds_max(const float* v) {
 
 
 
-// Window of nw <= 64 candidates in S.wkey: top-k / top-p threshold (order key
-// of the value), computed by the calling wave.  Returns false when the window
-// does not reach the top-p mass.  Also returns each lane's window entry (key)
-// and its mass (e).  Each lane counts the entries at or above its own and sums
-// their masses, reading the window with broadcast LDS loads (keys are unique).
+// Window of nw <= 128 candidates (win: order key of the value in the high word,
+// ~index in the low word, so keys are unique): top-k / top-p threshold (order
+// key of the value), computed by the calling wave.  Entry q sits in lane q & 63,
+// slot q >> 6.  Returns false when the window does not reach the top-p mass.
+// Also returns each slot's entry (key) and its mass (e).  Each slot counts the
+// entries at or above its own and sums their masses, reading the window with
+// broadcast LDS loads.
 template <int NT>
 __device__ __forceinline__ bool small_window(Smem<NT>& S, const uint64_t* win, int nw, bool kon, int32_t k,
                                              bool pon, float p, double Z, const Ex& X, uint32_t* tkey,
-                                             uint64_t* key, float* e) {
+                                             uint64_t (&key)[2], float (&e)[2]) {
   const int lane = threadIdx.x & 63;
-  const bool in = lane < nw;
-  const uint64_t mine = in ? win[lane] : 0ull;
-  const uint32_t kx = (uint32_t)(mine >> 32);
-  const float em = in ? X.e(okey_inv(kx)) : 0.0f;
-  S.we[lane] = em;
-  int cnt = 0;       // entries at or above mine
-  double pre = 0.0;  // their mass
+  bool in[2];
+  uint64_t mine[2];
+  uint32_t kx[2];
+  float em[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = lane + h * kWave;
+    in[h] = q < nw;
+    mine[h] = in[h] ? win[q] : 0ull;
+    kx[h] = (uint32_t)(mine[h] >> 32);
+    em[h] = in[h] ? X.e(okey_inv(kx[h])) : 0.0f;
+    S.we[q] = em[h];
+  }
+  int cnt[2] = {0, 0};         // entries at or above the slot's
+  double pre[2] = {0.0, 0.0};  // their mass
   for (int q0 = 0; q0 < nw; q0 += 8) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int q = q0 + i;
       const uint64_t other = win[q];
       const float eo = S.we[q];
-      const bool ge = q < nw && other >= mine;
-      cnt += ge ? 1 : 0;
-      pre += ge ? (double)eo : 0.0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool ge = q < nw && other >= mine[h];
+        cnt[h] += ge ? 1 : 0;
+        pre[h] += ge ? (double)eo : 0.0;
+      }
     }
   }
+  // key of the slot flagged in ballot b0 (slot 0) or else b1 (slot 1)
+  auto pick = [&](uint64_t b0, uint64_t b1) -> uint32_t {
+    return b0 ? (uint32_t)__builtin_amdgcn_readlane((int)kx[0], __ffsll((unsigned long long)b0) - 1)
+              : (uint32_t)__builtin_amdgcn_readlane((int)kx[1], __ffsll((unsigned long long)b1) - 1);
+  };
   uint32_t th = 0u;  // keep values with key >= th
   double ZK = Z;
   if (kon) {
-    const uint64_t b = __ballot(in && cnt == (k <= nw ? k : nw));  // the k-th largest
-    if (!b) return false;
-    th = (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)b) - 1);
-    ZK = wave_sum(in && kx >= th ? (double)em : 0.0);
+    const int target = k <= nw ? k : nw;  // the k-th largest
+    const uint64_t b0 = __ballot(in[0] && cnt[0] == target), b1 = __ballot(in[1] && cnt[1] == target);
+    if (!b0 && !b1) return false;
+    th = pick(b0, b1);
+    ZK = wave_sum((in[0] && kx[0] >= th ? (double)em[0] : 0.0) + (in[1] && kx[1] >= th ? (double)em[1] : 0.0));
   }
   if (pon) {
-    const bool hit = in && kx >= th && pre >= (double)p * ZK;
-    const int r = wave_min_i(hit ? cnt : 0x7fffffff);
-    const uint64_t b = __ballot(hit && cnt == r);
-    if (!b) return false;
-    th = (uint32_t)__builtin_amdgcn_readlane((int)kx, __ffsll((unsigned long long)b) - 1);
+    bool hit[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) hit[h] = in[h] && kx[h] >= th && pre[h] >= (double)p * ZK;
+    const int r = wave_min_i(min(hit[0] ? cnt[0] : 0x7fffffff, hit[1] ? cnt[1] : 0x7fffffff));
+    const uint64_t b0 = __ballot(hit[0] && cnt[0] == r), b1 = __ballot(hit[1] && cnt[1] == r);
+    if (!b0 && !b1) return false;
+    th = pick(b0, b1);
   }
   *tkey = th;
-  *key = mine;
-  *e = em;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    key[h] = mine[h];
+    e[h] = em[h];
+  }
   return true;
 }
 
@@ -1400,43 +1437,58 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   const int bq_incl = wave_incl_scan_i(cq, lane);
   const int nw = bin >= 0 ? __builtin_amdgcn_readlane(bq_incl, NW - 1) : 0x7fffffff;
   const bool ovf = __ballot(lane < NW && cq > Smem<NT>::kSeg) != 0;
-  if (nw <= kWave && !ovf) {
+  if (nw <= 2 * kWave && !ovf) {
     // The window reaches the top-k count / top-p mass (bin test above), so
-    // wave 0 finishes the row alone.
+    // wave 0 finishes the row alone, from LDS (two entries per lane).
     if (wid != 0) return;
-    // gather entry `lane` of the window: segment w with base_w <= lane
-    int w = 0, bw = 0;
+    // gather window entries lane and lane + 64: segment w with base_w <= position
+    int w0 = 0, bw0 = 0, w1 = 0, bw1 = 0;
 #pragma unroll
     for (int q = 1; q < NW; ++q) {
       const int bq = __builtin_amdgcn_readlane(bq_incl - cq, q);
       if (lane >= bq) {
-        w = q;
-        bw = bq;
+        w0 = q;
+        bw0 = bq;
+      }
+      if (lane + kWave >= bq) {
+        w1 = q;
+        bw1 = bq;
       }
     }
-    const uint64_t ent = lane < nw ? S.stage[w * Smem<NT>::kSeg + (lane - bw)] : 0ull;
-    S.wwin[lane] = ent;
+    S.wwin[lane] = lane < nw ? S.stage[w0 * Smem<NT>::kSeg + (lane - bw0)] : 0ull;
+    S.wwin[lane + kWave] = lane + kWave < nw ? S.stage[w1 * Smem<NT>::kSeg + (lane + kWave - bw1)] : 0ull;
     uint32_t tkey;
-    uint64_t key;
-    float e;
-    if (!small_window<NT>(S, S.wwin, nw, kon, A.k, pon, A.p, Z, X, &tkey, &key, &e)) tkey = 0u;  // unreachable
-    // inverse CDF over the kept entries (key >= tkey); lanes are in index order
-    const bool in = lane < nw && (uint32_t)(key >> 32) >= tkey;
-    const int32_t idx = (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffu));
-    const float ek = in ? e : 0.0f;
-    const double pre = wave_incl_scan((double)ek, lane);
-    const double total = readlane_d(pre, 63);
+    uint64_t key[2];
+    float e[2];
+    if (!small_window<NT>(S, S.wwin, nw, kon, A.k, pon, A.p, Z, X, &tkey, key, e)) tkey = 0u;  // unreachable
+    // inverse CDF over the kept entries (key >= tkey), in index order: slot 0
+    // of lanes 0..63, then slot 1
+    float ek[2];
+    int32_t idx[2];
+    bool in[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      in[h] = lane + h * kWave < nw && (uint32_t)(key[h] >> 32) >= tkey;
+      idx[h] = (int32_t)(0xffffffffu - (uint32_t)(key[h] & 0xffffffffu));
+      ek[h] = in[h] ? e[h] : 0.0f;
+    }
+    const double pre0 = wave_incl_scan((double)ek[0], lane);
+    const double pre1 = wave_incl_scan((double)ek[1], lane) + readlane_d(pre0, 63);
+    const double total = readlane_d(pre1, 63);
     float u = A.u;
     asm volatile("" : "+s"(u));
     const double U = (double)u * total;
-    const uint64_t cross = __ballot(ek > 0.0f && pre > U);
-    const uint64_t pos = __ballot(ek > 0.0f);
-    const uint64_t kept = __ballot(in);
-    int src;
-    if (cross) src = __ffsll((unsigned long long)cross) - 1;
-    else if (pos) src = 63 - __clzll((long long)pos);           // u >= 1 or rounding: last with mass
-    else src = kept ? 63 - __clzll((long long)kept) : 0;
-    const int id = __builtin_amdgcn_readlane(idx, src);
+    const uint64_t c0 = __ballot(ek[0] > 0.0f && pre0 > U), c1 = __ballot(ek[1] > 0.0f && pre1 > U);
+    const uint64_t p0 = __ballot(ek[0] > 0.0f), p1 = __ballot(ek[1] > 0.0f);
+    const uint64_t k0 = __ballot(in[0]), k1 = __ballot(in[1]);
+    int src = 0, h = 0;
+    if (c0) src = __ffsll((unsigned long long)c0) - 1;
+    else if (c1) src = __ffsll((unsigned long long)c1) - 1, h = 1;
+    else if (p1) src = 63 - __clzll((long long)p1), h = 1;  // u >= 1 or rounding: last with mass
+    else if (p0) src = 63 - __clzll((long long)p0);
+    else if (k1) src = 63 - __clzll((long long)k1), h = 1;
+    else if (k0) src = 63 - __clzll((long long)k0);
+    const int id = __builtin_amdgcn_readlane(h ? idx[1] : idx[0], src);
     if (lane == 0) *out = id;
     return;
   }
@@ -1508,14 +1560,17 @@ void sampler_kernel(SampleParams P) {
     if (threadIdx.x == 0) P.out[b] = -1;
     return;
   }
+  // The arguments' loads go out before the row's and are made wave-uniform
+  // after it: converting right away would wait a full memory round trip
+  // before the row is requested.
   RowArgs A{};
-  if (!GREEDY) A = row_args(P, r);
+  if (!GREEDY) A = row_args_load(P, r);
   Row<T, NT, CAP, VEC, FULL> R;
   R.init(P.logits, r, P.ld, P.V, cmax);
   R.fetch();
   if (GREEDY) row_greedy(R, &P.out[b], S);
-  else if (R.nstream() <= CAP) row_sample_fused(R, A, &P.out[b], S, csum);
-  else row_sample(R, A, &P.out[b], S, csum);
+  else if (R.nstream() <= CAP) row_sample_fused(R, uniform(A), &P.out[b], S, csum);
+  else row_sample(R, uniform(A), &P.out[b], S, csum);
 }
 
 // ---------------------------------------------------------------------------

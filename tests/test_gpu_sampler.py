@@ -268,3 +268,82 @@ def test_sampler_prepare_and_sample(lsg, orc, dev):
     args.uniforms = None
     a = s.sample(x, args)
     assert ((a >= 0) & (a < 3000)).all()
+
+
+# ------------------------------------------- large batches (B > 2 x CUs) ----
+def _mixed_params(B, V, g, dev):
+    """Per-row modes cycling through greedy-in-batch (T=1e-6), no filter,
+    top-k, top-p, top-k + top-p, k=1 and k >= V."""
+    T = 0.3 + torch.rand(B, generator=g, device=dev)
+    T[0::7] = 1e-6
+    K = torch.tensor([-1, -1, 20, -1, 50, 1, V + 1], dtype=torch.int32, device=dev).repeat(B // 7 + 1)[:B]
+    P = torch.tensor([1.0, 1.0, 1.0, 0.9, 0.95, 1.0, 0.8], device=dev).repeat(B // 7 + 1)[:B]
+    U = torch.rand(B, generator=g, device=dev)
+    return T, K.contiguous(), P.contiguous(), U
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 65536), (torch.float16, 65536), (torch.bfloat16, 40000),
+                                     (torch.float32, 32768), (torch.float32, 20001), (torch.bfloat16, 49152)])
+def test_large_batches(lsg, orc, dev, dtype, V):
+    """B=600 rows: more workgroups than two per CU, so rows run in successive
+    waves of workgroups; mixed modes per row, ragged and full rows."""
+    g = torch.Generator(device=dev).manual_seed(V + 17)
+    B = 600
+    x = (torch.randn(B, V, generator=g, device=dev) * 3).to(dtype)
+    x[5, 100] = float("nan")
+    x[9, :] = float("-inf")
+    x[9, V - 1] = 2.0
+    T, K, P, U = _mixed_params(B, V, g, dev)
+    check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.05)
+    check_sampling(lsg, orc, x, T, None, None, U, max_amb_frac=0.05)
+    ids = lsg.sample_rows(x, None, None, None, None)
+    assert torch.equal(ids.long(), torch.argmax(x, -1))
+
+
+def test_large_gather_and_count(lsg, orc, dev):
+    """Large batch with row_idx (invalid entries -> -1) and a device row count
+    below B_out: rows past the count stay untouched."""
+    g = torch.Generator(device=dev).manual_seed(23)
+    Bs, V = 700, 65536
+    x = (torch.randn(Bs, V, generator=g, device=dev) * 2).to(torch.bfloat16)
+    T, K, P, U = _mixed_params(Bs, V, g, dev)
+    perm = torch.randperm(Bs, generator=g, device=dev).to(torch.int32)[:640].contiguous()
+    perm[3] = -5
+    perm[300] = Bs + 1
+    full = lsg.sample_rows(x, T, K, P, U)
+    out = torch.full((640,), -7, dtype=torch.int32, device=dev)
+    lsg.sample_rows(x, T, K, P, U, row_idx=perm, out=out)
+    pi = perm.long().cpu()
+    valid = (pi >= 0) & (pi < Bs)
+    got = out.cpu()
+    assert torch.equal(got[valid], full.cpu()[pi[valid]])
+    assert (got[~valid] == -1).all()
+    out.fill_(-7)
+    n = torch.tensor([555], dtype=torch.int32, device=dev)
+    lsg.sample_rows(x, None, None, None, None, row_idx=perm, n_rows=n, out=out)
+    got = out.cpu()
+    am = torch.argmax(x, -1).to(torch.int32).cpu()
+    v = valid[:555]
+    assert torch.equal(got[:555][v], am[pi[:555][v]])
+    assert (got[:555][~v] == -1).all() and (got[555:] == -7).all()
+
+
+def test_large_graph_replay(lsg, dev):
+    """A 520-row top-p launch captured in a HIP graph: every replay matches eager."""
+    wl = lsg.workloads.sample_huginn(dev, B=520)
+    args = (wl["logits"], wl["temperatures"], None, wl["top_p"], wl["uniforms"])
+    eager = lsg.sample_rows(*args).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lsg.sample_rows(*args)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = lsg.sample_rows(*args)
+    for i in range(3):
+        out.fill_(-1)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
