@@ -292,7 +292,8 @@ struct Smem {
   uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass as float bits)
   uint32_t kmin;           // smallest order key in the candidate window
   unsigned long long rbins[4][kRefBins + 1];  // exact refinement: bin copies by lane, one bin apart in bank order
-  float we[2 * kWave];     // small window: masses
+  int rk_cnt[2 * kWave];    // small window: entries at or above each entry
+  unsigned long long rk_fix[2 * kWave];  // and their mass, 2^-40 fixed point
   static constexpr int kSeg = kWave;     // candidates staged per wave
   union {
     uint64_t stage[NW * kSeg];  // per-wave candidate segments, in index order
@@ -305,7 +306,6 @@ struct Smem {
   double rZ;               // row normaliser, histogram bin and candidate floor,
   int rbin;                // derived by wave 0 for the whole workgroup
   float rxlo;
-  uint64_t wwin[2 * kWave];  // small window, in index order
   int wn;
   int pick;
 };
@@ -994,47 +994,15 @@ __device__ __forceinline__ float lds_max(const float* v) {
 
 
 
-// Window of nw <= 128 candidates (win: order key of the value in the high word,
-// ~index in the low word, so keys are unique): top-k / top-p threshold (order
-// key of the value), computed by the calling wave.  Entry q sits in lane q & 63,
-// slot q >> 6.  Returns false when the window does not reach the top-p mass.
-// Also returns each slot's entry (key) and its mass (e).  Each slot counts the
-// entries at or above its own and sums their masses, reading the window with
-// broadcast LDS loads.
-template <int NT>
-__device__ __forceinline__ bool small_window(Smem<NT>& S, const uint64_t* win, int nw, bool kon, int32_t k,
-                                             bool pon, float p, double Z, const Ex& X, uint32_t* tkey,
-                                             uint64_t (&key)[2], float (&e)[2]) {
-  const int lane = threadIdx.x & 63;
-  bool in[2];
-  uint64_t mine[2];
-  uint32_t kx[2];
-  float em[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = lane + h * kWave;
-    in[h] = q < nw;
-    mine[h] = in[h] ? win[q] : 0ull;
-    kx[h] = (uint32_t)(mine[h] >> 32);
-    em[h] = in[h] ? X.e(okey_inv(kx[h])) : 0.0f;
-    S.we[q] = em[h];
-  }
-  int cnt[2] = {0, 0};         // entries at or above the slot's
-  double pre[2] = {0.0, 0.0};  // their mass
-  for (int q0 = 0; q0 < nw; q0 += 8) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int q = q0 + i;
-      const uint64_t other = win[q];
-      const float eo = S.we[q];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bool ge = q < nw && other >= mine[h];
-        cnt[h] += ge ? 1 : 0;
-        pre[h] += ge ? (double)eo : 0.0;
-      }
-    }
-  }
+// Threshold of a window of nw <= 128 candidates (order key of the value in the
+// high word of each entry, ~index in the low word, so keys are unique), from
+// each entry's rank: cnt = entries at or above it, pre = their mass.  Entry q
+// sits in lane q & 63, slot q >> 6 of the calling wave.  Returns the top-k /
+// top-p threshold as the order key of the value (keep key >= it), or false
+// when the window does not reach the top-k count / top-p mass.
+__device__ __forceinline__ bool window_pick(const bool (&in)[2], const uint32_t (&kx)[2], const float (&em)[2],
+                                            const int (&cnt)[2], const double (&pre)[2], int nw, bool kon,
+                                            int32_t k, bool pon, float p, double Z, uint32_t* tkey) {
   // key of the slot flagged in ballot b0 (slot 0) or else b1 (slot 1)
   auto pick = [&](uint64_t b0, uint64_t b1) -> uint32_t {
     return b0 ? (uint32_t)__builtin_amdgcn_readlane((int)kx[0], __ffsll((unsigned long long)b0) - 1)
@@ -1059,11 +1027,6 @@ __device__ __forceinline__ bool small_window(Smem<NT>& S, const uint64_t* win, i
     th = pick(b0, b1);
   }
   *tkey = th;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    key[h] = mine[h];
-    e[h] = em[h];
-  }
   return true;
 }
 
@@ -1364,6 +1327,10 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
   }
   __syncthreads();
+  if (t < 2 * kWave) {  // small-window ranks (accumulated after the next barrier)
+    S.rk_cnt[t] = 0;
+    S.rk_fix[t] = 0ull;
+  }
   const double Z = uni(S.rZ);
   constexpr int SH = KeyShift<T>::value;
   int bin = uni(S.rbin);
@@ -1438,10 +1405,11 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   const int nw = bin >= 0 ? __builtin_amdgcn_readlane(bq_incl, NW - 1) : 0x7fffffff;
   const bool ovf = __ballot(lane < NW && cq > Smem<NT>::kSeg) != 0;
   if (nw <= 2 * kWave && !ovf) {
-    // The window reaches the top-k count / top-p mass (bin test above), so
-    // wave 0 finishes the row alone, from LDS (two entries per lane).
-    if (wid != 0) return;
-    // gather window entries lane and lane + 64: segment w with base_w <= position
+    // The window reaches the top-k count / top-p mass (bin test above).  Every
+    // wave holds the whole window (entries lane and lane + 64, in index order)
+    // and ranks it against its own segment; counts and masses (2^-40 fixed
+    // point: exact, independent of the order of the LDS atomics) add up in
+    // LDS.  Wave 0 then thresholds and walks it alone.
     int w0 = 0, bw0 = 0, w1 = 0, bw1 = 0;
 #pragma unroll
     for (int q = 1; q < NW; ++q) {
@@ -1455,22 +1423,62 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
         bw1 = bq;
       }
     }
-    S.wwin[lane] = lane < nw ? S.stage[w0 * Smem<NT>::kSeg + (lane - bw0)] : 0ull;
-    S.wwin[lane + kWave] = lane + kWave < nw ? S.stage[w1 * Smem<NT>::kSeg + (lane + kWave - bw1)] : 0ull;
+    bool in[2];
+    uint64_t mine[2];
+    uint32_t kx[2];
+    float em[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q = lane + h * kWave;
+      in[h] = q < nw;
+      mine[h] = in[h] ? S.stage[(h ? w1 : w0) * Smem<NT>::kSeg + (q - (h ? bw1 : bw0))] : 0ull;
+      kx[h] = (uint32_t)(mine[h] >> 32);
+      em[h] = in[h] ? X.e(okey_inv(kx[h])) : 0.0f;
+    }
+    {
+      const int cw = __builtin_amdgcn_readlane(cq, wid);
+      const uint64_t* seg = S.stage + wid * Smem<NT>::kSeg;
+      int cnt[2] = {0, 0};
+      unsigned long long fix[2] = {0ull, 0ull};
+      for (int i = 0; i < cw; ++i) {
+        const uint64_t other = seg[i];
+        const unsigned long long eo =
+            (unsigned long long)((double)X.e(okey_inv((uint32_t)(other >> 32))) * kFix);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bool ge = other >= mine[h];
+          cnt[h] += ge ? 1 : 0;
+          fix[h] += ge ? eo : 0ull;
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (in[h] && cnt[h] > 0) {
+          atomicAdd(&S.rk_cnt[lane + h * kWave], cnt[h]);
+          atomicAdd(&S.rk_fix[lane + h * kWave], fix[h]);
+        }
+    }
+    __syncthreads();
+    if (wid != 0) return;
+    int cnt[2];
+    double pre[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      cnt[h] = in[h] ? S.rk_cnt[lane + h * kWave] : 0;
+      pre[h] = in[h] ? (double)S.rk_fix[lane + h * kWave] * (1.0 / kFix) : 0.0;
+    }
     uint32_t tkey;
-    uint64_t key[2];
-    float e[2];
-    if (!small_window<NT>(S, S.wwin, nw, kon, A.k, pon, A.p, Z, X, &tkey, key, e)) tkey = 0u;  // unreachable
+    if (!window_pick(in, kx, em, cnt, pre, nw, kon, A.k, pon, A.p, Z, &tkey)) tkey = 0u;  // unreachable
     // inverse CDF over the kept entries (key >= tkey), in index order: slot 0
     // of lanes 0..63, then slot 1
     float ek[2];
     int32_t idx[2];
-    bool in[2];
+    bool kept[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      in[h] = lane + h * kWave < nw && (uint32_t)(key[h] >> 32) >= tkey;
-      idx[h] = (int32_t)(0xffffffffu - (uint32_t)(key[h] & 0xffffffffu));
-      ek[h] = in[h] ? e[h] : 0.0f;
+      kept[h] = in[h] && kx[h] >= tkey;
+      idx[h] = (int32_t)(0xffffffffu - (uint32_t)(mine[h] & 0xffffffffu));
+      ek[h] = kept[h] ? em[h] : 0.0f;
     }
     const double pre0 = wave_incl_scan((double)ek[0], lane);
     const double pre1 = wave_incl_scan((double)ek[1], lane) + readlane_d(pre0, 63);
@@ -1480,7 +1488,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     const double U = (double)u * total;
     const uint64_t c0 = __ballot(ek[0] > 0.0f && pre0 > U), c1 = __ballot(ek[1] > 0.0f && pre1 > U);
     const uint64_t p0 = __ballot(ek[0] > 0.0f), p1 = __ballot(ek[1] > 0.0f);
-    const uint64_t k0 = __ballot(in[0]), k1 = __ballot(in[1]);
+    const uint64_t k0 = __ballot(kept[0]), k1 = __ballot(kept[1]);
     int src = 0, h = 0;
     if (c0) src = __ffsll((unsigned long long)c0) - 1;
     else if (c1) src = __ffsll((unsigned long long)c1) - 1, h = 1;
