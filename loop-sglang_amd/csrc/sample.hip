@@ -77,6 +77,17 @@ __device__ __forceinline__ float mul_up(float a, float b) {
   return __uint_as_float(1u);
 }
 
+// floor(e * 2^40) for a mass e in [0, 1], from its bits: the 24-bit
+// significand shifted by the exponent (no double-precision conversion; zero
+// and denormal masses, below 2^-126, give 0).
+__device__ __forceinline__ unsigned long long fix40(float e) {
+  const uint32_t b = __float_as_uint(e);
+  const int E = (int)(b >> 23) - 110;  // e = m * 2^(E - 40), m the significand
+  const unsigned long long m = (unsigned long long)((b & 0x7fffffu) | 0x800000u);
+  if (b < 0x00800000u || E <= -24) return 0ull;
+  return E >= 0 ? (m << E) : (m >> -E);
+}
+
 // Exponent map of one row: e(x) = 2^y(x), y(x) = (x - m) * c with c = log2(e)/T.
 // When |m*c| < 2^22, y is one fma against b = m*c rounded up: every exponent is
 // then <= 0 and all of them carry the same offset m*c - b in [-1/2, 0], which
@@ -1071,7 +1082,7 @@ __device__ __forceinline__ bool refine_threshold(R_& R, const Ex& X, double ZK, 
                         if (x == x && key >= lo_ && key < hi_) {
                           const int b = (int)((hi_ - 1u - key) >> sh);
                           const unsigned long long add =
-                              kon ? 1ull : (unsigned long long)((double)X.e(x) * kFix + 0.5);
+                              kon ? 1ull : fix40(X.e(x));
                           atomicAdd(&mine[b], add);
                         }
                       }
@@ -1443,7 +1454,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       for (int i = 0; i < cw; ++i) {
         const uint64_t other = seg[i];
         const unsigned long long eo =
-            (unsigned long long)((double)X.e(okey_inv((uint32_t)(other >> 32))) * kFix);
+            fix40(X.e(okey_inv((uint32_t)(other >> 32))));
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const bool ge = other >= mine[h];
