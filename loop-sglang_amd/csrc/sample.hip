@@ -1454,7 +1454,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       for (int i = 0; i < cw; ++i) {
         const uint64_t other = seg[i];
         const unsigned long long eo =
-            fix40(X.e(okey_inv((uint32_t)(other >> 32))));
+            (unsigned long long)((double)X.e(okey_inv((uint32_t)(other >> 32))) * kFix);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const bool ge = other >= mine[h];
