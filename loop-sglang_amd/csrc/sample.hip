@@ -1596,6 +1596,7 @@ void sampler_kernel(SampleParams P) {
 // Host launch.  One workgroup per output row; rows past the device row count
 // (n_rows_dev) exit at once.
 //   chunks per row NV <= 256*8    256 threads, 8 chunks each in registers
+//   NV == 1024*6 (e.g. 49152 bf16) 1024 threads, exactly 6 full chunks each
 //   NV <= 1024*8                  1024 threads, 8 chunks each (two per CU)
 //   NV <= 1024*16                 1024 threads, 16 chunks each (one per CU)
 //   longer rows                   1024 threads, 16 chunks each, the rest streamed
@@ -1613,6 +1614,7 @@ static void launch_rows(const SampleParams& P, bool vec, hipStream_t st) {
   if (!vec) launch(sampler_kernel<G, T, 1024, 16, false, kStream, 4>, 1024, P, st);
   else if (NV <= 256 * 8) launch(sampler_kernel<G, T, 256, 8, true, kBounded, 8>, 256, P, st);
   else if (NV == 1024 * 8 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 8, true, kFull, 8>, 1024, P, st);
+  else if (NV == 1024 * 6 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 6, true, kFull, 8>, 1024, P, st);
   else if (NV <= 1024 * 8) launch(sampler_kernel<G, T, 1024, 8, true, kBounded, 8>, 1024, P, st);
   else if (NV == 1024 * 16 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 16, true, kFull, 4>, 1024, P, st);
   else if (NV <= 1024 * 16) launch(sampler_kernel<G, T, 1024, 16, true, kBounded, 4>, 1024, P, st);

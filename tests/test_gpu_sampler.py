@@ -283,7 +283,8 @@ def _mixed_params(B, V, g, dev):
 
 
 @pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 65536), (torch.float16, 65536), (torch.bfloat16, 40000),
-                                     (torch.float32, 32768), (torch.float32, 20001), (torch.bfloat16, 49152)])
+                                     (torch.float32, 32768), (torch.float32, 20001), (torch.bfloat16, 49152),
+                                     (torch.float16, 49152), (torch.float32, 24576)])
 def test_large_batches(lsg, orc, dev, dtype, V):
     """B=600 rows: more workgroups than two per CU, so rows run in successive
     waves of workgroups; mixed modes per row, ragged and full rows."""
