@@ -31,6 +31,7 @@ COMMON = [
 
 SOURCES = {
     "sample.hip": ["-ffp-contract=fast"],
+    "sample_quad.hip": ["-ffp-contract=fast"],
     "exit_gate.hip": ["-ffp-contract=off"],
     "capi.hip": [],
 }

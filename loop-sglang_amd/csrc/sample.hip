@@ -26,6 +26,7 @@
 // ~1e-7 relative.
 #include "lsg_capi_internal.h"
 #include "lsg_common.h"
+#include "lsg_sample.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -47,18 +48,6 @@ constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
 // float sums (at most 2048 terms: < 2^-13 relative) and of the per-wave
 // reference shifts (< 2^-17 relative per term).
 constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
-
-struct SampleParams {
-  const void* logits;
-  int64_t B_src, V, ld, B_out;
-  const float* temps;
-  const int32_t* top_k;
-  const float* top_p;
-  const float* uniforms;
-  const int32_t* row_idx;
-  const int32_t* n_rows_dev;
-  int32_t* out;
-};
 
 // exp2 clamped to [0, 1]; the clamp folds into v_exp_f32 and maps NaN (from a
 // NaN logit) to 0.
@@ -1661,6 +1650,7 @@ extern "C" int lsg_sample(const void* logits, int dtype, int64_t B_src, int64_t 
                  row_idx, n_rows_dev, out_ids};
   const bool greedy = temperatures == nullptr;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (quad_sample_launch(P, dtype, greedy, vec, st)) return check_launch("lsg_sample");
   int rc;
   if (dtype == kF32) rc = launch_dtype<float>(P, greedy, vec, st);
   else if (dtype == kBF16) rc = launch_dtype<bf16_t>(P, greedy, vec, st);

@@ -1,0 +1,1090 @@
+// Token sampling with one four-wave workgroup per row (the row held in registers).
+//
+// Replaces, for the decode token path of Loop-SGLang:
+//   Sampler.sample            python/loopsgl/model_executor/sample.py:107-112
+//   torch.argmax (greedy)     sample.py:110-111 (+ int32 cast, model_runner.py:279-280)
+//   sample_impl -> flashinfer softmax / *_sampling_from_probs   sample.py:60-81
+// for rows of exactly 256 * CAP 16-byte chunks (V = 65536 or 49152 for bf16/fp16,
+// 32768 or 24576 for fp32); sample.hip serves every other shape with the same
+// semantics:
+//   T <= 0 or non-finite, or max x non-finite  -> id = argmax (torch rules)
+//   m = max x (NaN ignored), e_i = 2^((x_i - m) * log2(e)/T)
+//   K = {x >= k-th largest x} if 1 <= k < V            (ties kept)
+//   P = {x in K : x >= tau}, tau = largest x with mass(x >= tau) >= p * mass(K)
+//   id = first index j in P (ascending) with cumsum_P(e)[j] > u * sum_P(e)
+//
+// Structure (one row per 256-thread workgroup, three resident per CU):
+//   * every lane issues all of its CAP nontemporal 128-bit loads at once; wave w
+//     owns chunks [w*CAP*64, (w+1)*CAP*64), its j-th load reads the 64 chunks
+//     (w*CAP + j)*64 + lane (1 KiB contiguous), so index order is (wave, j, lane,
+//     element);
+//   * one pass over the chunks as they arrive: a running maximum per lane with
+//     the masses rescaled whenever it rises (e = 2^((x - max) c) is exact near
+//     the maximum, whatever the data), the lane's two largest chunk maxima and a
+//     16-bit upper bound of every chunk maximum (to LDS);
+//   * barrier 1: the row maximum and normaliser from four wave summaries;
+//     unfiltered rows walk the inverse CDF right away (crossing wave, lane, chunk,
+//     element);
+//   * top-k / top-p rows: a histogram of the lanes' two largest chunk maxima
+//     (distinct elements) bounds the threshold from below; every wave stages its
+//     elements above the bound in index order; barrier 2; one wave finishes the
+//     window (<= 256 entries) with a 1/8-binary-order histogram, an exact
+//     resolution inside the crossing bin and the walk.  Larger windows take an
+//     exact radix refinement over the row.
+// Sums above the chunk level are float64; window masses are 2^-40 fixed point,
+// so the threshold sums are exact and independent of atomic order.
+#include "lsg_capi_internal.h"
+#include "lsg_common.h"
+#include "lsg_sample.h"
+
+#include <type_traits>
+
+namespace lsg {
+namespace quad {
+
+constexpr int kNT = 256;          // threads per row
+constexpr int kNW = kNT / kWave;  // waves per row
+constexpr int kHB = 128;          // coarse histogram: bins of 1/4 binary order over y in [-32, 0]
+constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order over y in [-32, 0]
+constexpr int kSeg = 128;         // window entries staged per wave
+constexpr int kWin = 256;         // window finished by one wave (4 entries per lane)
+constexpr int kRB = 256;          // refinement bins per level
+constexpr double kFix = 1099511627776.0;  // 2^40
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kNonTemporal = 2;   // buffer-load cache policy: stream through the caches
+// Top-p bin test margin: the bin is chosen where the float sums of the binned
+// chunk maxima reach p*Z*(1 + 2^-10), so the window always reaches p*Z despite
+// the rounding of those sums.
+constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
+
+// 2^y clamped to [0, 1]: folds into v_exp_f32's clamp, NaN -> 0.
+__device__ __forceinline__ float ex2c(float y) {
+  return __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(y), 0.0f, 1.0f);
+}
+// IEEE maximum (NaN-propagating, no operand canonicalisation): v_maximum3_f32.
+__device__ __forceinline__ float fmx(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// floor(e * 2^40) for a mass e in [0, 1], from its bits (exact).
+__device__ __forceinline__ unsigned long long fix40(float e) {
+  const uint32_t b = __float_as_uint(e);
+  const int E = (int)(b >> 23) - 110;
+  const unsigned long long m = (unsigned long long)((b & 0x7fffffu) | 0x800000u);
+  if (b < 0x00800000u || E <= -24) return 0ull;
+  return E >= 0 ? (m << E) : (m >> -E);
+}
+
+// Upper bound of a float as a bf16 bit pattern (exact for bf16 values).
+__device__ __forceinline__ uint32_t bf16_up(float m) {
+  const uint32_t b = __float_as_uint(m);
+  return (b & 0x80000000u) ? (b >> 16) : ((b + 0xffffu) >> 16);
+}
+
+// A 16-byte chunk as one 128-bit register tuple.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// Elements of a 16-byte chunk as floats.
+template <typename T>
+struct QE;
+template <>
+struct QE<bf16_t> {
+  static constexpr int EPV = 8, SH = 16;
+  __device__ static __forceinline__ void unpack(const v4u& v, float (&x)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = __uint_as_float(w[k] << 16);
+      x[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct QE<f16_t> {
+  static constexpr int EPV = 8, SH = 13;
+  __device__ static __forceinline__ void unpack(const v4u& v, float (&x)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] & 0xffffu));
+      x[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] >> 16));
+    }
+  }
+};
+template <>
+struct QE<float> {
+  static constexpr int EPV = 4, SH = 0;
+  __device__ static __forceinline__ void unpack(const v4u& v, float (&x)[4]) {
+    x[0] = __uint_as_float(v.x);
+    x[1] = __uint_as_float(v.y);
+    x[2] = __uint_as_float(v.z);
+    x[3] = __uint_as_float(v.w);
+  }
+};
+
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&e)[N]) {
+#pragma unroll
+  for (int w = 1; w < N; w <<= 1)
+#pragma unroll
+    for (int i = 0; i < N; i += 2 * w) e[i] += e[i + w];
+  return e[0];
+}
+
+template <int CAP>
+struct Smem {
+  uint32_t cm[kNT][CAP / 2 + 1];  // chunk-maximum upper bounds, two 16-bit patterns per word (odd stride: no bank conflicts)
+  uint32_t wh[kNW][kHB];      // per-wave coarse histograms (count, or mass as float bits)
+  union {
+    struct {                                      // top-k / top-p window
+      uint64_t seg[kNW][kSeg];                    // window entries per wave, index order
+      unsigned long long fmass[kFB];              // fine histogram: masses (2^-40 fixed point)
+      uint32_t fcnt[kFB];                         // fine histogram: counts
+      v4u stg[kNW][kWave];                        // staged candidate chunks per wave, (column, lane) order
+      uint32_t smeta[kNW][kWave];                 // their column * 64 + lane
+    };
+    struct {                                      // exact refinement and its inverse CDF
+      unsigned long long rb[4][kRB + 1];          // refinement bins, four copies by lane
+      double colsum[kNW][CAP];                    // kept mass per wave and chunk column
+    };
+  };
+  float wmax[kNW];
+  double wz[kNW];
+  double red[kNW];
+  int cnt[kNW];
+  int imin;
+};
+
+// A row in registers: CAP chunks per lane, wave-blocked.
+template <typename T, int CAP>
+struct Row {
+  static constexpr int EPV = QE<T>::EPV;
+  v4u d[CAP];
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t c0;  // chunk index of this lane's load j = 0
+  __device__ __forceinline__ void init(const void* logits, int64_t r, int64_t ld, uint32_t V) {
+    const char* base = reinterpret_cast<const char*>(logits) + r * ld * (int64_t)sizeof(T);
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)(V * (uint32_t)sizeof(T)),
+                                           0x00020000);
+    c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)(CAP * kWave) + (threadIdx.x & 63);
+  }
+  __device__ __forceinline__ void fetch() {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j)
+      d[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(c0 * 16u), j * kWave * 16, kNonTemporal);
+  }
+  // Chunk `chunk` of the row re-read from memory (cold paths: the register
+  // copy is then no longer needed, so those paths add no register pressure).
+  __device__ __forceinline__ v4u load_at(uint32_t chunk) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(chunk * 16u), 0, 0);
+  }
+  __device__ __forceinline__ v4u load(int j) const { return load_at(c0 + (uint32_t)j * kWave); }
+  __device__ __forceinline__ uint32_t elem(int j, int i) const { return (c0 + (uint32_t)j * kWave) * EPV + i; }
+  // Mark the chunks as possibly changed, so that values unpacked from them in an
+  // earlier phase are recomputed instead of kept live (which would double the
+  // registers the row needs).
+  __device__ __forceinline__ void launder() const {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) asm volatile("" : "+v"(const_cast<v4u&>(d[j])));
+  }
+};
+
+// Chunk-maximum upper bound j of this thread, from LDS.
+template <int CAP>
+__device__ __forceinline__ float cm_at(const Smem<CAP>& S, int j) {
+  const uint32_t w = S.cm[threadIdx.x][j >> 1];
+  return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+
+// f(j, chunk, keep) over this lane's chunks re-read from memory, eight loads
+// in flight at a time; chunks whose maximum bound fails keep() in every lane of
+// the wave are skipped (and not loaded by the lanes that fail it).
+template <typename T, int CAP, class K, class F>
+__device__ __forceinline__ void each_chunk_mem(const Row<T, CAP>& R, const Smem<CAP>& S, K&& keep, F&& f) {
+  static_assert(CAP % 8 == 0, "chunks are re-read in groups of eight");
+#pragma unroll 1
+  for (int jb = 0; jb < CAP; jb += 8) {
+    v4u v[8];
+    bool kp[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      kp[q] = keep(cm_at(S, jb + q));
+      v[q] = kp[q] ? R.load(jb + q) : v4u{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (__ballot(kp[q])) f(jb + q, v[q], kp[q]);
+  }
+}
+
+struct LaneStats {
+  float ml, t1, t2;  // running maximum, two largest chunk maxima
+  double S;          // mass relative to ml
+};
+
+// The pass over the lane's chunks (all loads already issued): running maximum,
+// masses rescaled to it, two largest chunk maxima, chunk-maximum bounds to LDS.
+// NANIGN: NaN elements are ignored (a second pass for rows holding NaN);
+// otherwise NaN propagates into the maximum and marks the row for that pass.
+template <bool NANIGN, typename T, int CAP>
+__device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP>& S) {
+  constexpr int EPV = QE<T>::EPV;
+  LaneStats s{-INFINITY, -INFINITY, -INFINITY, 0.0};
+  uint32_t pk = 0;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    float x[EPV];
+    // NANIGN (rare rows holding NaN): chunks re-read from memory, so this pass
+    // adds no register pressure to the register-resident row
+    QE<T>::unpack(NANIGN ? R.load(j) : R.d[j], x);
+    float cm = x[0];
+#pragma unroll
+    for (int i = 1; i < EPV; ++i) cm = NANIGN ? fmaxf(cm, x[i]) : fmx(cm, x[i]);
+    const float mn = NANIGN ? fmaxf(s.ml, cm) : fmx(s.ml, cm);
+    const float f = ex2c((s.ml - mn) * c);
+    // masses in two halves of EPV/2 (fewer values live at once)
+    float e[EPV / 2];
+#pragma unroll
+    for (int i = 0; i < EPV / 2; ++i) e[i] = ex2c((x[i] - mn) * c);
+    float cs = tree_sum(e);
+    asm volatile("" : "+v"(cs));
+#pragma unroll
+    for (int i = 0; i < EPV / 2; ++i) e[i] = ex2c((x[EPV / 2 + i] - mn) * c);
+    cs += tree_sum(e);
+    s.S = __builtin_fma(s.S, (double)f, (double)cs);
+    s.ml = mn;
+    const float ct = NANIGN ? (cm == cm ? cm : -INFINITY) : cm;
+    s.t2 = __builtin_amdgcn_fmed3f(s.t1, s.t2, ct);
+    s.t1 = fmx(s.t1, ct);
+    const uint32_t h = bf16_up(cm);
+    if (j & 1) S.cm[threadIdx.x][j >> 1] = pk | (h << 16);
+    else pk = h;
+    // materialise the running state here (not sunk to its first use, which
+    // would keep every chunk's operands live), one chunk at a time
+    asm volatile("" : "+v"(s.ml), "+v"(s.t1), "+v"(s.t2), "+v"(s.S), "+v"(pk));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return s;
+}
+
+// Maximum pass only (argmax): NaN-propagating lane maximum and the first chunk
+// at which it was reached (for NaN: the first chunk holding a NaN).
+template <bool MEM, typename T, int CAP>
+__device__ __forceinline__ float lane_max(const Row<T, CAP>& R, int* fj) {
+  constexpr int EPV = QE<T>::EPV;
+  float ml = -INFINITY;
+  int f = 0;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    float x[EPV];
+    QE<T>::unpack(MEM ? R.load(j) : R.d[j], x);
+    float cm = x[0];
+#pragma unroll
+    for (int i = 1; i < EPV; ++i) cm = fmx(cm, x[i]);
+    f = (cm > ml || (cm != cm && ml == ml)) ? j : f;
+    ml = fmx(ml, cm);
+    asm volatile("" : "+v"(ml), "+v"(f));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  *fj = f;
+  return ml;
+}
+
+// Sum of one double per wave over the workgroup, in wave order (all waves call).
+template <int CAP>
+__device__ __forceinline__ double wg_sum(Smem<CAP>& S, double wv) {
+  if ((threadIdx.x & 63) == 0) S.red[threadIdx.x >> 6] = wv;
+  __syncthreads();
+  const double r = ((S.red[0] + S.red[1]) + S.red[2]) + S.red[3];
+  __syncthreads();
+  return r;
+}
+
+// torch.argmax over the row (first maximum; the first NaN if any): every wave calls.
+// MEM: the chunks are re-read from memory (a rare path of the sampling kernel).
+template <bool MEM, typename T, int CAP>
+__device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP>& S, int32_t* out) {
+  constexpr int EPV = QE<T>::EPV;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int fj;
+  const float ml = lane_max<MEM>(R, &fj);
+  const float wm = wave_maximum(ml);
+  __syncthreads();  // earlier readers of S are done
+  if (threadIdx.x == 0) S.imin = 0x7fffffff;
+  if (lane == 0) S.wmax[wid] = wm;
+  __syncthreads();
+  const float m = uni(fmx(fmx(S.wmax[0], S.wmax[1]), fmx(S.wmax[2], S.wmax[3])));
+  const bool isn = m != m;
+  const bool cand = isn ? (ml != ml) : (ml == m);
+  // the chunk where this lane first reached the maximum (from registers:
+  // masked ORs, no dynamic register indexing)
+  v4u v = {0u, 0u, 0u, 0u};
+  if constexpr (MEM) {
+    v = R.load(fj);
+  } else {
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      const uint32_t mk = 0u - (uint32_t)(fj == j);
+      v.x |= R.d[j].x & mk;
+      v.y |= R.d[j].y & mk;
+      v.z |= R.d[j].z & mk;
+      v.w |= R.d[j].w & mk;
+    }
+  }
+  float x[EPV];
+  QE<T>::unpack(v, x);
+  int first = 0x7fffffff;
+#pragma unroll
+  for (int i = EPV - 1; i >= 0; --i) {
+    const bool hit = (int)isn ? (x[i] != x[i]) : (x[i] == m);
+    first = hit ? (int)R.elem(fj, i) : first;
+  }
+  first = cand ? first : 0x7fffffff;
+  const int wf = wave_min_i(first);
+  if (lane == 0 && wf != 0x7fffffff) atomicMin(&S.imin, wf);
+  __syncthreads();
+  if (threadIdx.x == 0) *out = S.imin;
+}
+
+// Inverse CDF in index order (wave, chunk column j, lane, element) over
+// kept masses.  The crossing wave of U = u * Z comes from the waves' masses Zq
+// (identical in every wave); the others return.  Sets *Uw (mass to go from
+// the start of the crossing wave).
+__device__ __forceinline__ int cross_wave(const double (&Zq)[kNW], float u, double* Uw) {
+  const double Z = ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3];
+  const double U = (double)uni(u) * Z;
+  int ws = -1, wl = 0;
+  double acc = 0.0, bw = 0.0, bl = 0.0;
+#pragma unroll
+  for (int q = 0; q < kNW; ++q) {
+    if (Zq[q] > 0.0) {
+      wl = q;
+      bl = acc;
+    }
+    if (ws < 0 && acc + Zq[q] > U) {
+      ws = q;
+      bw = acc;
+    }
+    acc += Zq[q];
+  }
+  if (ws < 0) {  // u >= 1 or rounding: the last wave with mass
+    ws = wl;
+    bw = bl;
+  }
+  *Uw = U - bw;
+  return ws;
+}
+
+// In the crossing wave ws, with the crossing column js (colex: the wave's mass
+// in the columns before it): v is this lane's chunk of column js; finds the
+// lane, then the element, and writes the id.
+template <typename T, int CAP, class EM>
+__device__ __forceinline__ void finish_column(const v4u& v, int ws, int js, double colex, double Uw, EM&& emass,
+                                              int32_t* out) {
+  constexpr int EPV = QE<T>::EPV;
+  const int lane = threadIdx.x & 63;
+  float x[EPV], em[EPV];
+  QE<T>::unpack(v, x);
+  double lm = 0.0;
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    em[i] = emass(x[i]);
+    lm += (double)em[i];
+  }
+  const double inc = colex + wave_incl_scan(lm, lane);
+  const double exc = inc - lm;
+  int ls;
+  {
+    const uint64_t hit = __ballot(lm > 0.0 && inc > Uw);
+    const uint64_t pos = __ballot(lm > 0.0);
+    ls = hit ? __ffsll((unsigned long long)hit) - 1 : (pos ? 63 - __clzll((long long)pos) : 0);
+  }
+  if (lane == ls) {
+    double a = exc;
+    int pick = -1, last = -1;
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      if (em[i] > 0.0f) {
+        last = i;
+        a += (double)em[i];
+        if (pick < 0 && a > Uw) pick = i;
+      }
+    }
+    if (pick < 0) pick = last < 0 ? 0 : last;
+    *out = (int32_t)(((uint32_t)(ws * CAP + js) * kWave + (uint32_t)ls) * EPV + pick);
+  }
+}
+
+// Unfiltered rows: the crossing wave re-reads its chunks from memory, eight
+// columns in flight at a time, sums the columns in order until U is crossed,
+// then finishes that column.  (The register copy of the row is left to the
+// top-k / top-p path, which needs it on every row.)
+template <typename T, int CAP, class EM>
+__device__ __forceinline__ void walk_cols(const Row<T, CAP>& R, const double (&Zq)[kNW], float u, EM&& emass,
+                                          int32_t* out) {
+  constexpr int EPV = QE<T>::EPV;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  double Uw;
+  const int ws = cross_wave(Zq, u, &Uw);
+  if (wid != ws) return;
+  double acc = 0.0, accl = 0.0;
+  int js = -1, jl = 0;
+#pragma unroll 1
+  for (int jb = 0; jb < CAP && js < 0; jb += 8) {
+    v4u v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = R.load(jb + q);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (js < 0) {
+        float x[EPV], e[EPV];
+        QE<T>::unpack(v[q], x);
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) e[i] = emass(x[i]);
+        const double C = wave_sum((double)tree_sum(e));
+        if (C > 0.0) {
+          jl = jb + q;
+          accl = acc;
+        }
+        if (acc + C > Uw) js = jb + q;
+        else acc += C;
+      }
+    }
+  }
+  if (js < 0) {  // rounding: the last column with mass
+    js = jl;
+    acc = accl;
+  }
+  finish_column<T, CAP>(R.load(js), ws, js, acc, Uw, emass, out);
+}
+
+// Bitwise OR over the wave (identical in every lane).
+__device__ __forceinline__ uint32_t wave_or(uint32_t v) {
+  v |= (uint32_t)dpp_i<0x128>(0, (int)v);
+  v |= (uint32_t)dpp_i<0x124>(0, (int)v);
+  v |= (uint32_t)dpp_i<0x122>(0, (int)v);
+  v |= (uint32_t)dpp_i<0x121>(0, (int)v);
+  return (uint32_t)(__builtin_amdgcn_readlane((int)v, 0) | __builtin_amdgcn_readlane((int)v, 16) |
+                    __builtin_amdgcn_readlane((int)v, 32) | __builtin_amdgcn_readlane((int)v, 48));
+}
+
+// Smallest value with order key >= kk (keys below -inf's are NaN patterns).
+__device__ __forceinline__ float key_value(uint32_t kk) {
+  return kk <= okey(-INFINITY) ? -INFINITY : okey_inv(kk);
+}
+
+// Exact top-k (count target) or top-p (mass target, 2^-40 fixed point) threshold
+// by radix refinement over order keys (okey(x) >> SH) of the members: non-NaN
+// elements with y(x) >= Lm and x >= xmin.  Each level splits the bracket
+// [lo, hi) holding the boundary into 256 bins (one LDS atomic per member, four
+// bin copies picked by lane); the scan from the top with the totals above the
+// bracket picks the bin; down to one key (ties kept).  Every wave calls.
+template <typename T, int CAP>
+__device__ __forceinline__ bool refine(const Row<T, CAP>& R, Smem<CAP>& S, float m, float c, float Lm, float xmin, bool kon,
+                       double target, uint32_t* thr_key) {
+  constexpr int EPV = QE<T>::EPV, SH = QE<T>::SH;
+  const int t = threadIdx.x, lane = t & 63;
+  uint32_t lo = okey(xmin) >> SH, hi = (okey(m) >> SH) + 1u;
+  double above = 0.0;
+  for (int level = 0; level < 8; ++level) {
+    if (hi <= lo) return false;
+    int sh = 0;
+    while (((hi - lo - 1u) >> sh) >= (uint32_t)kRB) ++sh;
+    for (int i = t; i < 4 * (kRB + 1); i += kNT) (&S.rb[0][0])[i] = 0ull;
+    __syncthreads();
+    const uint32_t lo_ = lo, hi_ = hi;
+    const float xlo = key_value(lo << SH);
+    unsigned long long* mine = S.rb[lane & 3];
+    each_chunk_mem(R, S, [&](float cb) { return cb >= xlo && (cb - m) * c >= Lm; },
+                   [&](int, const v4u& v, bool may) {
+                     float x[EPV];
+                     QE<T>::unpack(v, x);
+#pragma unroll
+                     for (int i = 0; i < EPV; ++i) {
+                       const uint32_t key = okey(x[i]) >> SH;
+                       const float y = (x[i] - m) * c;
+                       if (may && x[i] == x[i] && x[i] >= xmin && y >= Lm && key >= lo_ && key < hi_)
+                         atomicAdd(&mine[(hi_ - 1u - key) >> sh], kon ? 1ull : fix40(ex2c(y)));
+                     }
+                   });
+    __syncthreads();
+    double bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int bi = 4 * lane + q;
+      bv[q] = (double)(S.rb[0][bi] + S.rb[1][bi] + S.rb[2][bi] + S.rb[3][bi]);
+    }
+    const double ls = (bv[0] + bv[1]) + (bv[2] + bv[3]);
+    const double incl = wave_incl_scan(ls, lane);
+    const uint64_t bal = __ballot(above + incl >= target);
+    __syncthreads();  // every wave has read the bins
+    if (!bal) return false;
+    const int lb = __ffsll((unsigned long long)bal) - 1;
+    double a = above + readlane_d(incl - ls, lb);
+    int bs = 4 * lb + 3;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const double vq = readlane_d(bv[q], lb);
+      if (a + vq >= target) {
+        bs = 4 * lb + q;
+        break;
+      }
+      a += vq;
+    }
+    above = a;
+    const uint32_t nhi = hi - ((uint32_t)bs << sh);
+    const uint32_t nlo = nhi - lo > (1u << sh) ? nhi - (1u << sh) : lo;
+    lo = nlo;
+    hi = nhi;
+    if (hi - lo == 1u) {
+      *thr_key = lo << SH;
+      return true;
+    }
+  }
+  return false;
+}
+
+// Fallback for top-k / top-p rows without a usable window: exact refinement,
+// then the inverse CDF over {x >= thr} with fresh masses.  Every wave calls.
+template <typename T, int CAP>
+__device__ __forceinline__ void row_exact(const Row<T, CAP>& R, Smem<CAP>& S, float m, float c, double Z, bool kon, int32_t k,
+                          bool pon, float p, float Lm, float u, int32_t* out) {
+  constexpr int EPV = QE<T>::EPV;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  float thr = -INFINITY;
+  uint32_t tk;
+  if (kon) {
+    if (refine(R, S, m, c, Lm, -INFINITY, true, (double)k, &tk)) thr = key_value(tk);
+  }
+  if (pon) {
+    double ZK = Z;
+    if (kon) {
+      double acc = 0.0;
+      each_chunk_mem(R, S, [&](float cb) { return cb >= thr; }, [&](int, const v4u& v, bool keep) {
+        float x[EPV];
+        QE<T>::unpack(v, x);
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) acc += (keep && x[i] >= thr) ? (double)ex2c((x[i] - m) * c) : 0.0;
+      });
+      ZK = wg_sum(S, wave_sum(acc));
+    }
+    // members below 2^-40 of the maximum weigh < 2^-24 of Z altogether
+    const float Lp = fmaxf(Lm, -40.0f);
+    if (refine(R, S, m, c, Lp, thr, false, (double)p * ZK * kFix, &tk)) thr = fmaxf(thr, key_value(tk));
+  }
+  auto emass = [&](float x) { return x >= thr ? ex2c((x - m) * c) : 0.0f; };
+  // kept mass per chunk column of this wave (columns no lane keeps stay 0)
+  if (lane < CAP) S.colsum[wid][lane] = 0.0;
+  each_chunk_mem(R, S, [&](float cb) { return cb >= thr; }, [&](int j, const v4u& v, bool keep) {
+    float x[EPV];
+    QE<T>::unpack(v, x);
+    float e[EPV];
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) e[i] = keep ? emass(x[i]) : 0.0f;
+    const double C = wave_sum((double)tree_sum(e));
+    if (lane == 0) S.colsum[wid][j] = C;
+  });
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const double cs = lane < CAP ? S.colsum[wid][lane] : 0.0;
+  const double cinc = wave_incl_scan(cs, lane);
+  if (lane == 63) S.wz[wid] = cinc;
+  __syncthreads();
+  const double Zq[kNW] = {S.wz[0], S.wz[1], S.wz[2], S.wz[3]};
+  double Uw;
+  const int ws = cross_wave(Zq, u, &Uw);
+  if (wid != ws) return;
+  int js;
+  {
+    const uint64_t hit = __ballot(cs > 0.0 && cinc > Uw);
+    const uint64_t pos = __ballot(cs > 0.0);
+    js = hit ? __ffsll((unsigned long long)hit) - 1 : (pos ? 63 - __clzll((long long)pos) : 0);
+  }
+  const double colex = readlane_d(cinc - cs, js);
+  finish_column<T, CAP>(R.load(js), ws, js, colex, Uw, emass, out);
+}
+
+// Entry ranked r-th largest (1-based) among the window entries of one fine bin
+// (flag `inb` per slot); keys are unique.  Wave 0 only.
+__device__ __forceinline__ uint64_t bin_rank(const uint64_t (&key)[4], const bool (&inb)[4], int r) {
+  uint64_t best = 0ull;
+  bool done = false;
+#pragma unroll 1
+  for (int h = 0; h < 4 && !done; ++h) {
+    uint64_t b = __ballot(inb[h]);
+    while (b && !done) {
+      const int l = __ffsll((unsigned long long)b) - 1;
+      b &= b - 1;
+      const uint64_t kq = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key[h] >> 32), l) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)(key[h] & 0xffffffffu), l);
+      int gt = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) gt += (inb[g] && key[g] > kq) ? 1 : 0;
+      if (wave_sum_i(gt) == r - 1) {
+        best = kq;
+        done = true;
+      }
+    }
+  }
+  return best;
+}
+
+// Window finish by wave 0: entries q = h*64 + lane (h = 0..3) of the window
+// (nw <= 256, index order).  Threshold from the fine histograms, exact inside
+// the crossing bin; then the inverse CDF over the kept entries.
+template <int CAP>
+__device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&cq)[kNW], float m, float c, double Z, bool kon,
+                              int32_t k, bool pon, float p, float u, int32_t* out) {
+  const int lane = threadIdx.x & 63;
+  int base[kNW];
+  base[0] = 0;
+#pragma unroll
+  for (int q = 1; q < kNW; ++q) base[q] = base[q - 1] + cq[q - 1];
+  bool in[4];
+  uint64_t key[4];
+  uint32_t kx[4];
+  float e[4];
+  int fb[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int q = 4 * lane + h;  // lane-major: lane l holds window positions 4l .. 4l+3
+    in[h] = q < nw;
+    int w = 0;
+#pragma unroll
+    for (int g = 1; g < kNW; ++g) w = q >= base[g] ? g : w;
+    key[h] = in[h] ? S.seg[w][q - base[w]] : 0ull;
+    kx[h] = (uint32_t)(key[h] >> 32);
+    const float x = okey_inv(kx[h]);
+    const float y = (x - m) * c;
+    e[h] = in[h] ? ex2c(y) : 0.0f;
+    fb[h] = in[h] ? min(kFB - 1, (int)(-8.0f * y)) : 0;
+  }
+  uint32_t thr = 0u;  // keep entries with value key >= thr
+  double ZK = Z;
+  // Cumulative fine-bin totals from the top: lane l owns bins 4l .. 4l+3.
+  auto crossing = [&](const double (&bv)[4], double target, int* bin, double* above) -> bool {
+    const double ls = (bv[0] + bv[1]) + (bv[2] + bv[3]);
+    const double incl = wave_incl_scan(ls, lane);
+    const uint64_t bal = __ballot(incl >= target);
+    if (!bal) return false;
+    const int lb = __ffsll((unsigned long long)bal) - 1;
+    double a = readlane_d(incl - ls, lb);
+    int bs = 4 * lb + 3;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const double vq = readlane_d(bv[q], lb);
+      if (a + vq >= target) {
+        bs = 4 * lb + q;
+        break;
+      }
+      a += vq;
+    }
+    *bin = bs;
+    *above = a;
+    return true;
+  };
+  bool inK[4] = {in[0], in[1], in[2], in[3]};
+  if (kon) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) S.fcnt[4 * lane + q] = 0u;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (in[h]) atomicAdd(&S.fcnt[fb[h]], 1u);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    double bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = (double)S.fcnt[4 * lane + q];
+    int bk;
+    double above;
+    const int kk = k < nw ? k : nw;
+    if (crossing(bv, (double)kk, &bk, &above)) {
+      bool inb[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) inb[h] = in[h] && fb[h] == bk;
+      const uint64_t kth = bin_rank(key, inb, kk - (int)above);
+      thr = (uint32_t)(kth >> 32);
+    }
+    double zk = 0.0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      inK[h] = in[h] && kx[h] >= thr;
+      zk += inK[h] ? (double)e[h] : 0.0;
+    }
+    ZK = wave_sum(zk);
+  }
+  if (pon) {
+    const double target = (double)p * ZK * kFix;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) S.fmass[4 * lane + q] = 0ull;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (inK[h]) atomicAdd(&S.fmass[fb[h]], fix40(e[h]));
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    double bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = (double)S.fmass[4 * lane + q];
+    int bp;
+    double above;
+    if (crossing(bv, target, &bp, &above)) {
+      // distinct value keys of the crossing bin, from the top, until the target is met
+      bool rem[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) rem[h] = inK[h] && fb[h] == bp;
+      double a = above;
+      uint32_t t2 = thr;
+#pragma unroll 1
+      for (int it = 0; it < kWin; ++it) {
+        uint32_t mk = 0u;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) mk = max(mk, rem[h] ? kx[h] : 0u);
+        const uint32_t vmax = (uint32_t)wave_max_i((int)(mk ^ 0x80000000u)) ^ 0x80000000u;
+        if (vmax == 0u) break;
+        double s = 0.0;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const bool eq = rem[h] && kx[h] == vmax;
+          s += eq ? (double)fix40(e[h]) : 0.0;
+          rem[h] = rem[h] && !eq;
+        }
+        a += wave_sum(s);
+        t2 = vmax;
+        if (a >= target) break;
+      }
+      thr = max(thr, t2);
+    }
+  }
+  // inverse CDF over the kept entries in index order (positions 4l .. 4l+3 in lane l)
+  float ek[4];
+  bool kept[4];
+  double ls = 0.0;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    kept[h] = inK[h] && kx[h] >= thr;
+    ek[h] = kept[h] ? e[h] : 0.0f;
+    ls += (double)ek[h];
+  }
+  const double inc = wave_incl_scan(ls, lane);
+  const double U = (double)uni(u) * readlane_d(inc, 63);
+  int src;
+  {
+    const uint64_t hit = __ballot(ls > 0.0 && inc > U);
+    const uint64_t pos = __ballot(ls > 0.0);
+    const uint64_t any = __ballot(kept[0] || kept[1] || kept[2] || kept[3]);
+    src = hit ? __ffsll((unsigned long long)hit) - 1
+              : (pos ? 63 - __clzll((long long)pos) : (any ? 63 - __clzll((long long)any) : 0));
+  }
+  if (lane == src) {
+    double a = inc - ls;
+    int pick = -1, lastm = -1, lastk = 0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      if (kept[h]) lastk = h;
+      if (ek[h] > 0.0f) {
+        lastm = h;
+        a += (double)ek[h];
+        if (pick < 0 && a > U) pick = h;
+      }
+    }
+    if (pick < 0) pick = lastm >= 0 ? lastm : lastk;
+    uint32_t lo = 0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (h == pick) lo = (uint32_t)(key[h] & 0xffffffffu);
+    *out = (int32_t)(0xffffffffu - lo);
+  }
+}
+
+// The waves' masses in the row frame (maximum m), recomputed from the published
+// wave summaries wherever needed (identical in every wave; keeping them live
+// across the tail would cost registers the row needs).
+template <int CAP>
+__device__ __forceinline__ void wave_masses(const Smem<CAP>& S, float m, float c, double (&Zq)[kNW]) {
+#pragma unroll
+  for (int q = 0; q < kNW; ++q) Zq[q] = S.wz[q] * (double)ex2c((S.wmax[q] - m) * c);
+}
+
+// Row statistics after the pass, published per wave before barrier 1.
+template <typename T, int CAP>
+__device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, bool pon, Smem<CAP>& S) {
+  constexpr int N = CAP * QE<T>::EPV;  // elements per lane
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const float wm = wave_maximum(s.ml);
+  const double sl = s.S * (double)ex2c((s.ml - wm) * c);  // this lane's mass, wave frame
+  const double wz = wave_sum(sl);
+  if (kon || pon) {
+    // two largest chunk maxima of each lane (distinct elements), wave frame
+    uint32_t* h = S.wh[wid];
+    const float y1 = (s.t1 - wm) * c, y2 = (s.t2 - wm) * c;
+    if (y1 >= -32.0f) {
+      const int b = min(kHB - 1, (int)(-4.0f * y1));
+      if (kon) atomicAdd(&h[b], 1u);
+      else atomicAdd(reinterpret_cast<float*>(&h[b]), ex2c(y1));
+    }
+    if (y2 >= -32.0f) {
+      const int b = min(kHB - 1, (int)(-4.0f * y2));
+      if (kon) atomicAdd(&h[b], 1u);
+      else atomicAdd(reinterpret_cast<float*>(&h[b]), ex2c(y2));
+    }
+    if (!kon) {
+      // The lane's other N - 2 elements weigh R: at any level L at or below
+      // y_e = log2(R / (2 (N - 2))) those at or above L weigh at least
+      // R - (N - 2) 2^L >= R / 2, so R / 2 counts at y_e.
+      const float rest = (float)(sl - (double)ex2c(y1) - (double)ex2c(y2));
+      const float ye = rest > 0.0f ? __log2f(rest * (0.5f / (float)(N - 2))) : -INFINITY;
+      if (ye >= -32.0f) atomicAdd(reinterpret_cast<float*>(&h[min(kHB - 1, (int)(-4.0f * ye))]), 0.5f * rest);
+    }
+  }
+  if (lane == 0) {
+    S.wmax[wid] = wm;
+    S.wz[wid] = wz;
+  }
+}
+
+template <typename T, int CAP>
+__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3)))
+void quad_sample_kernel(SampleParams P) {
+  constexpr int EPV = QE<T>::EPV;
+  __shared__ Smem<CAP> S;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  int64_t nrows = P.B_out;
+  if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
+  const int64_t b = blockIdx.x;
+  if (b >= nrows) return;
+  const int64_t r = P.row_idx ? (int64_t)uni((int)P.row_idx[b]) : b;
+  if (r < 0 || r >= P.B_src) {
+    if (threadIdx.x == 0) P.out[b] = -1;
+    return;
+  }
+  int32_t* out = &P.out[b];
+  // Per-row arguments: issued before the row (the in-order load counter then
+  // waits for them alone), through buffer resources that read 0 for an absent
+  // array.
+  const uint32_t ab = (uint32_t)min<int64_t>(P.B_src * 4, 0x7fffffff);
+  auto arg = [&](const void* a) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a), (short)0, a ? (int)ab : 0, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(r * 4), 0, 0);
+  };
+  const uint32_t aT = arg(P.temps), aU = arg(P.uniforms), aK = arg(P.top_k), aP = arg(P.top_p);
+  Row<T, CAP> R;
+  R.init(P.logits, r, P.ld, (uint32_t)P.V);
+  R.fetch();
+  const float Tr = __uint_as_float(uni(aT));
+  const float u = __uint_as_float(uni(aU));
+  const int32_t k = (int32_t)uni(aK);
+  const float p = __uint_as_float(uni(aP) | (P.top_p ? 0u : 0x3f800000u));  // absent: 0 | bits of 1.0
+  const bool tvalid = Tr > 0.0f && Tr < INFINITY;
+  const float c = tvalid ? kLog2e / Tr : 1.0f;
+  const bool kon = k >= 1 && (int64_t)k < P.V, pon = p < 1.0f;
+  float wq[kNW] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY;
+  if (tvalid) {
+    if (kon || pon) S.wh[wid][lane] = S.wh[wid][lane + kWave] = 0u;  // this wave's histogram (a wave's LDS ops stay in order)
+    publish<T, CAP>(lane_pass<false>(R, c, S), c, kon, pon, S);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kNW; ++q) wq[q] = uni(S.wmax[q]);
+    m = fmx(fmx(wq[0], wq[1]), fmx(wq[2], wq[3]));
+    if (m != m) {
+      // NaN present: NaN carries no mass; pass again ignoring it
+      __syncthreads();
+      if (kon || pon) S.wh[wid][lane] = S.wh[wid][lane + kWave] = 0u;
+      publish<T, CAP>(lane_pass<true>(R, c, S), c, kon, pon, S);
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kNW; ++q) wq[q] = uni(S.wmax[q]);
+      m = fmaxf(fmaxf(wq[0], wq[1]), fmaxf(wq[2], wq[3]));
+    }
+  }
+  if (!tvalid || !(m > -INFINITY) || !(m < INFINITY)) {
+    row_argmax<true>(R, S, out);
+    return;
+  }
+  __builtin_amdgcn_s_setprio(2);
+  m = uni(m);
+  if (!kon && !pon) {
+    double Zq[kNW];
+    wave_masses(S, m, c, Zq);
+    walk_cols(R, Zq, u, [&](float x) { return ex2c((x - m) * c); }, out);
+    return;
+  }
+  // ---- top-k / top-p: floor from the merged histograms (row bin b gathers
+  // wave q's bin b - s_q, s_q = ceil(4 * (its shift below the row maximum));
+  // lane l holds row bins 2l and 2l + 1)
+  int bstar;
+  {
+    int pc[2] = {0, 0};
+    float pmf[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < kNW; ++q) {
+      const float D = (m - wq[q]) * c;
+      const int sq = D < 32.0f ? (int)__builtin_ceilf(4.0f * D + 0x1p-8f) : kHB;
+      const float fq = ex2c((wq[q] - m) * c);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int idx = 2 * lane + h - sq;
+        const uint32_t v = S.wh[q][idx < 0 ? 0 : idx];
+        if (idx >= 0) {
+          if (kon) pc[h] += (int)v;
+          else pmf[h] = __builtin_fmaf(__uint_as_float(v), fq, pmf[h]);
+        }
+      }
+    }
+    int lb = -1, hb = 1;
+    if (kon) {
+      const int inc = wave_incl_scan_i(pc[0] + pc[1], lane);
+      const uint64_t bal = __ballot(inc >= k);
+      if (bal) {
+        lb = __ffsll((unsigned long long)bal) - 1;
+        const int before = __builtin_amdgcn_readlane(inc - pc[0] - pc[1], lb);
+        hb = before + __builtin_amdgcn_readlane(pc[0], lb) >= k ? 0 : 1;
+      }
+    } else {
+      double Zq[kNW];
+      wave_masses(S, m, c, Zq);
+      const double tgt = (double)p * (((Zq[0] + Zq[1]) + Zq[2]) + Zq[3]) * kBinMargin;
+      const double inc = wave_incl_scan((double)pmf[0] + (double)pmf[1], lane);
+      const uint64_t bal = __ballot(inc >= tgt);
+      if (bal) {
+        lb = __ffsll((unsigned long long)bal) - 1;
+        const double before = readlane_d(inc - ((double)pmf[0] + (double)pmf[1]), lb);
+        hb = before + (double)readlane_f(pmf[0], lb) >= tgt ? 0 : 1;
+      }
+    }
+    bstar = lb < 0 ? -1 : 2 * lb + hb;
+  }
+  float Lm = -INFINITY;
+  if (bstar >= 0) {
+    Lm = -0.25f * (float)(bstar + 1) - 0x1p-8f;
+    // stage this wave's elements with y >= Lm, in index order (j, lane, element)
+    uint64_t* seg = S.seg[wid];
+    int run = 0;
+    // this lane's chunks whose maximum bound reaches the floor (all bound
+    // words read at once), and the columns where any lane has one
+    uint32_t hm = 0u;
+#pragma unroll
+    for (int q = 0; q < CAP / 2; ++q) {
+      const uint32_t w = S.cm[threadIdx.x][q];
+      hm |= ((__uint_as_float(w << 16) - m) * c >= Lm ? 1u : 0u) << (2 * q);
+      hm |= ((__uint_as_float(w & 0xffff0000u) - m) * c >= Lm ? 1u : 0u) << (2 * q + 1);
+    }
+    const uint32_t cols = uni(wave_or(hm));
+    // A: the lanes holding a candidate chunk copy it to this wave's staging
+    // area, column by column (slots in (column, lane) = index order)
+    v4u* stg = S.stg[wid];
+    uint32_t* meta = S.smeta[wid];
+    int ns = 0;
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      if ((cols >> j) & 1u) {
+        const bool hj = (hm >> j) & 1u;
+        const uint64_t bj = __ballot(hj);
+        const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
+        if (hj && slot < kWave) {
+          stg[slot] = R.d[j];
+          meta[slot] = (uint32_t)(j * kWave + lane);
+        }
+        ns += (int)__popcll(bj);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's staging writes are done
+    __builtin_amdgcn_wave_barrier();
+    // B: lane i takes staged chunk i and writes its elements above the floor
+    if (ns <= kWave) {
+      const bool act = lane < ns;
+      const v4u v = stg[act ? lane : 0];
+      const uint32_t mt = meta[act ? lane : 0];
+      const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);  // chunk index in the row
+      float x[EPV];
+      QE<T>::unpack(v, x);
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) cnt += (act && (x[i] - m) * c >= Lm) ? 1 : 0;
+      const int incl = wave_incl_scan_i(cnt, lane);
+      int pos = incl - cnt;
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        if (act && (x[i] - m) * c >= Lm) {
+          if (pos < kSeg) seg[pos] = ((uint64_t)okey(x[i]) << 32) | (uint64_t)(0xffffffffu - (ci * EPV + i));
+          ++pos;
+        }
+      }
+      run = __builtin_amdgcn_readlane(incl, 63);
+    } else {
+      run = kSeg + 1;  // too many candidate chunks: the exact path decides
+    }
+    if (lane == 0) S.cnt[wid] = run;
+  }
+  __syncthreads();
+  if (bstar >= 0) {
+    int cq[kNW], nw = 0;
+    bool ovf = false;
+#pragma unroll
+    for (int q = 0; q < kNW; ++q) {
+      cq[q] = uni(S.cnt[q]);
+      nw += cq[q];
+      ovf = ovf || cq[q] > kSeg;
+    }
+    if (!ovf && nw <= kWin) {
+      if (wid == 0) {
+        double Zq[kNW];
+        wave_masses(S, m, c, Zq);
+        window_finish(S, nw, cq, m, c, ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3], kon, k, pon, p, u, out);
+      }
+      return;
+    }
+  }
+  double Zq[kNW];
+  wave_masses(S, m, c, Zq);
+  row_exact(R, S, m, c, ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3], kon, k, pon, p, bstar >= 0 ? Lm : -INFINITY, u, out);
+}
+
+// All-greedy batch: torch.argmax per row.
+template <typename T, int CAP>
+__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3)))
+void quad_greedy_kernel(SampleParams P) {
+  __shared__ Smem<CAP> S;
+  int64_t nrows = P.B_out;
+  if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
+  const int64_t b = blockIdx.x;
+  if (b >= nrows) return;
+  const int64_t r = P.row_idx ? (int64_t)uni((int)P.row_idx[b]) : b;
+  if (r < 0 || r >= P.B_src) {
+    if (threadIdx.x == 0) P.out[b] = -1;
+    return;
+  }
+  Row<T, CAP> R;
+  R.init(P.logits, r, P.ld, (uint32_t)P.V);
+  R.fetch();
+  row_argmax<false>(R, S, &P.out[b]);
+}
+
+template <typename T, int CAP>
+static void launch(const SampleParams& P, bool greedy, hipStream_t st) {
+  if (greedy) hipLaunchKernelGGL((quad_greedy_kernel<T, CAP>), dim3((unsigned)P.B_out), dim3(kNT), 0, st, P);
+  else hipLaunchKernelGGL((quad_sample_kernel<T, CAP>), dim3((unsigned)P.B_out), dim3(kNT), 0, st, P);
+}
+
+template <typename T>
+static bool launch_dtype(const SampleParams& P, bool greedy, hipStream_t st) {
+  constexpr int EPV = QE<T>::EPV;
+  if (P.V % EPV != 0) return false;
+  const int64_t NV = P.V / EPV;
+  if (NV == (int64_t)kNT * 32) launch<T, 32>(P, greedy, st);
+  else if (NV == (int64_t)kNT * 24) launch<T, 24>(P, greedy, st);
+  else return false;
+  return true;
+}
+
+}  // namespace quad
+
+bool quad_sample_launch(const SampleParams& P, int dtype, bool greedy, bool vec, hipStream_t st) {
+  if (!vec) return false;
+  if (dtype == kF32) return quad::launch_dtype<float>(P, greedy, st);
+  if (dtype == kBF16) return quad::launch_dtype<bf16_t>(P, greedy, st);
+  if (dtype == kF16) return quad::launch_dtype<f16_t>(P, greedy, st);
+  return false;
+}
+
+}  // namespace lsg
