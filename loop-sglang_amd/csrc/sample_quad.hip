@@ -149,6 +149,8 @@ struct Smem {
   float wmax[kNW];
   double wz[kNW];
   double red[kNW];
+  double rz;
+  v4u lt[kNT];  // per lane: largest, second-largest chunk maximum, chunk of the largest
   int cnt[kNW];
   int imin;
 };
@@ -217,6 +219,7 @@ __device__ __forceinline__ void each_chunk_mem(const Row<T, CAP>& R, const Smem<
 
 struct LaneStats {
   float ml, t1, t2;  // running maximum, two largest chunk maxima
+  int j1;            // chunk holding t1
   double S;          // mass relative to ml
 };
 
@@ -227,7 +230,7 @@ struct LaneStats {
 template <bool NANIGN, typename T, int CAP>
 __device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP>& S) {
   constexpr int EPV = QE<T>::EPV;
-  LaneStats s{-INFINITY, -INFINITY, -INFINITY, 0.0};
+  LaneStats s{-INFINITY, -INFINITY, -INFINITY, 0, 0.0};
   uint32_t pk = 0;
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
@@ -253,13 +256,14 @@ __device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP
     s.ml = mn;
     const float ct = NANIGN ? (cm == cm ? cm : -INFINITY) : cm;
     s.t2 = __builtin_amdgcn_fmed3f(s.t1, s.t2, ct);
+    s.j1 = ct > s.t1 ? j : s.j1;
     s.t1 = fmx(s.t1, ct);
     const uint32_t h = bf16_up(cm);
     if (j & 1) S.cm[threadIdx.x][j >> 1] = pk | (h << 16);
     else pk = h;
     // materialise the running state here (not sunk to its first use, which
     // would keep every chunk's operands live), one chunk at a time
-    asm volatile("" : "+v"(s.ml), "+v"(s.t1), "+v"(s.t2), "+v"(s.S), "+v"(pk));
+    asm volatile("" : "+v"(s.ml), "+v"(s.t1), "+v"(s.t2), "+v"(s.j1), "+v"(s.S), "+v"(pk));
     __builtin_amdgcn_sched_barrier(0);
   }
   return s;
@@ -838,6 +842,7 @@ __device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, b
     S.wmax[wid] = wm;
     S.wz[wid] = wz;
   }
+  if (kon || pon) S.lt[threadIdx.x] = v4u{__float_as_uint(s.t1), __float_as_uint(s.t2), (uint32_t)s.j1, 0u};
 }
 
 template <typename T, int CAP>
@@ -942,7 +947,9 @@ void quad_sample_kernel(SampleParams P) {
     } else {
       double Zq[kNW];
       wave_masses(S, m, c, Zq);
-      const double tgt = (double)p * (((Zq[0] + Zq[1]) + Zq[2]) + Zq[3]) * kBinMargin;
+      const double Zr = ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3];
+      if (threadIdx.x == 0) S.rz = Zr;  // the row normaliser, for the window finish
+      const double tgt = (double)p * Zr * kBinMargin;
       const double inc = wave_incl_scan((double)pmf[0] + (double)pmf[1], lane);
       const uint64_t bal = __ballot(inc >= tgt);
       if (bal) {
@@ -961,12 +968,20 @@ void quad_sample_kernel(SampleParams P) {
     int run = 0;
     // this lane's chunks whose maximum bound reaches the floor (all bound
     // words read at once), and the columns where any lane has one
-    uint32_t hm = 0u;
+    // (a lane whose second-largest chunk maximum is below the floor has at
+    // most one such chunk, the one holding its largest; only lanes with more
+    // read their chunk bounds)
+    const v4u lt = S.lt[threadIdx.x];
+    const bool t2in = (__uint_as_float(lt.y) - m) * c >= Lm;
+    uint32_t hm = (__uint_as_float(lt.x) - m) * c >= Lm ? (1u << lt.z) : 0u;
+    if (__ballot(t2in) && t2in) {
+      hm = 0u;
 #pragma unroll
-    for (int q = 0; q < CAP / 2; ++q) {
-      const uint32_t w = S.cm[threadIdx.x][q];
-      hm |= ((__uint_as_float(w << 16) - m) * c >= Lm ? 1u : 0u) << (2 * q);
-      hm |= ((__uint_as_float(w & 0xffff0000u) - m) * c >= Lm ? 1u : 0u) << (2 * q + 1);
+      for (int q = 0; q < CAP / 2; ++q) {
+        const uint32_t w = S.cm[threadIdx.x][q];
+        hm |= ((__uint_as_float(w << 16) - m) * c >= Lm ? 1u : 0u) << (2 * q);
+        hm |= ((__uint_as_float(w & 0xffff0000u) - m) * c >= Lm ? 1u : 0u) << (2 * q + 1);
+      }
     }
     const uint32_t cols = uni(wave_or(hm));
     // A: the lanes holding a candidate chunk copy it to this wave's staging
@@ -1027,11 +1042,7 @@ void quad_sample_kernel(SampleParams P) {
       ovf = ovf || cq[q] > kSeg;
     }
     if (!ovf && nw <= kWin) {
-      if (wid == 0) {
-        double Zq[kNW];
-        wave_masses(S, m, c, Zq);
-        window_finish(S, nw, cq, m, c, ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3], kon, k, pon, p, u, out);
-      }
+      if (wid == 0) window_finish(S, nw, cq, m, c, (!kon && pon) ? S.rz : 0.0, kon, k, pon, p, u, out);
       return;
     }
   }
