@@ -91,8 +91,12 @@ int lsg_sample(const void* logits, int dtype, int64_t B_src, int64_t V, int64_t 
  *   keep_idx      i32[B] ascending rows with mask 0 (first B - *n_exit), or NULL.
  *   n_exit        i32[1] number of exited rows, or NULL.
  *   z_out         f32[B] gate logit after rounding to dtype, or NULL.
- *   workspace     >= lsg_workspace_bytes(LSG_OP_EXIT_GATE, B) bytes, zero-filled
- *                 before its first use; every call leaves it zero-filled again.
+ *   workspace     >= lsg_workspace_bytes(LSG_OP_EXIT_GATE, B) bytes, needed when
+ *                 exit_idx, keep_idx or n_exit is given; zero-filled once before
+ *                 its first use, then owned by the library (it keeps a call
+ *                 serial number there).  B < 2^30 with compaction.
+ * This is the --disable-lookahead-exit routing: a row's own gate routes it in the
+ * step it fires.  lsg_exit_gate_route adds the default (lookahead) timing.
  */
 int lsg_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh, const void* w,
                   const void* bias, const float* F_prev, float* F_next, const int32_t* slots,
@@ -100,6 +104,40 @@ int lsg_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh, c
                   int32_t min_loop_steps, int32_t lookahead, int32_t max_depth, uint8_t* mask,
                   int32_t* exit_idx, int32_t* keep_idx, int32_t* n_exit, float* z_out,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One core step of the Ouro gate with the scheduler's exit routing.  Replaces,
+ * besides what lsg_exit_gate replaces, the routing rules of CDBScheduler.
+ * _consume_gate and _run_core (managers/cdb_scheduler.py:207-222,254-266).
+ * Arguments as lsg_exit_gate, with mask = this step's gate signal (ouro.py:154,
+ * no depth cap) and the compaction taken over `route`:
+ *   disable_lookahead_exit  1: a row's request routes it in this step.
+ *                 0 (the scheduler's default): the request recorded for the row's
+ *                 state slot by the previous call on this workspace routes it (the
+ *                 token ran in consecutive core steps, so it advanced since its
+ *                 gate); this call's request is recorded for the next call.
+ *   pending       i64[n_slots] pending-gate pool, indexed like F (slots[row] or
+ *                 row), read and rewritten in place; opaque; zero-filled before
+ *                 first use.  A routed row's entry is cleared; a caller that
+ *                 moves a new token into a slot by other means (cancellation,
+ *                 retraction) writes 0 there.  May be NULL when
+ *                 disable_lookahead_exit = 1.
+ *   replay_depth  i32[B] or NULL: a value rd > 0 replaces the row's request by
+ *                 depth >= rd - (disable_lookahead_exit ? 0 : 1), depth =
+ *                 loop_step + 1 (cdb_scheduler.py:207-213).
+ *   route         u8[B] or NULL: 1 for rows routed to the coda in this step
+ *                 (request as above, or depth >= max_depth when max_depth > 0).
+ *   workspace     required (it carries the call serial number the pending pool
+ *                 is tagged with); one workspace per sequence of core steps.
+ */
+int lsg_exit_gate_route(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh,
+                        const void* w, const void* bias, const float* F_prev, float* F_next,
+                        const int32_t* slots, const int32_t* loop_step, int32_t loop_step_scalar,
+                        float tau, int32_t min_loop_steps, int32_t lookahead, int32_t max_depth,
+                        int32_t disable_lookahead_exit, int64_t* pending,
+                        const int32_t* replay_depth, uint8_t* mask, uint8_t* route,
+                        int32_t* exit_idx, int32_t* keep_idx, int32_t* n_exit, float* z_out,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * cumulative_exit_probability alone (models/looped/exit_gates.py:6-15):
@@ -114,7 +152,8 @@ int lsg_cumulative_exit_probability(const void* z, int dtype, const float* F_pre
  * ratio = ||h - h_prev||_2 / max(||h||_2, eps) in float32, mask = ratio < tau,
  * plus the same optional compaction outputs as lsg_exit_gate.
  * workspace: >= lsg_workspace_bytes(LSG_OP_REL_CHANGE, B) bytes (zero-filled
- * before first use) when exit_idx, keep_idx or n_exit is requested.
+ * before first use, then owned by the library) when exit_idx, keep_idx or n_exit
+ * is requested.
  */
 int lsg_relative_state_change(const void* h, const void* h_prev, int dtype, int64_t B, int64_t H,
                               int64_t ldh, int64_t ldp, float tau, float eps, float* ratio,

@@ -6,26 +6,30 @@ kernels in ``libloopsgl_tok.so`` (C ABI: include/loopsgl_tok.h):
   sampler      Sampler / BatchSamplingArgs / sample_impl  (model_executor/sample.py)
   exit_gate    OuroExitGate / HuginnExitGate / cumulative_exit_probability /
                relative_state_change                     (models/looped/*.py)
+               OuroExitGate.exit_route: the scheduler's exit routing
+                                                          (managers/cdb_scheduler.py)
+  integration  exit_signal / sample bindings for the reference's own model
+               and sampler objects
   decode_step  gate -> on-device exit compaction -> sampling of exited rows
-  core         SamplingParams / LoopParams               (core.py)
 
 The directory name contains a hyphen, so import it through
 ``__graft_entry__.package()`` (registers it as ``loop_sglang_amd``).
 """
-from .core import LoopParams, SamplingParams
 from .decode_step import DecodeStepResult, cdb_decode_step
 from .exit_gate import (
     GateResult,
+    RouteResult,
     HuginnExitGate,
     OuroExitGate,
     cumulative_exit_probability,
+    ouro_exit_signal,
     relative_state_change,
 )
 from .sampler import BatchSamplingArgs, Sampler, make_device_tensor, sample_impl, sample_rows
-from . import workloads
+from . import integration, workloads
 
 __all__ = [
-    "BatchSamplingArgs", "DecodeStepResult", "GateResult", "HuginnExitGate", "LoopParams",
-    "OuroExitGate", "Sampler", "SamplingParams", "cdb_decode_step", "cumulative_exit_probability",
+    "BatchSamplingArgs", "DecodeStepResult", "GateResult", "HuginnExitGate", "OuroExitGate",
+    "RouteResult", "Sampler", "cdb_decode_step", "cumulative_exit_probability", "integration", "ouro_exit_signal",
     "make_device_tensor", "relative_state_change", "sample_impl", "sample_rows",
 ]

@@ -25,6 +25,9 @@ SIGNATURES = {
     "lsg_sample": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P]),
     "lsg_exit_gate": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _F,
                                      _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "lsg_exit_gate_route": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32,
+                                           _F, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                           _SZ, _P]),
     "lsg_cumulative_exit_probability": (ctypes.c_int, [_P, ctypes.c_int, _P, _P, _I64, _P]),
     "lsg_relative_state_change": (ctypes.c_int, [_P, _P, ctypes.c_int, _I64, _I64, _I64, _I64, _F, _F, _P,
                                                  _P, _P, _P, _P, _P, _SZ, _P]),

@@ -30,10 +30,11 @@ extern "C" const char* lsg_last_error(void) { return lsg::g_err; }
 
 extern "C" int lsg_version(void) { return 1; }
 
-// Exit-compaction workspace: one arrival counter (padded to 256 B) followed by
-// a bitmask with one bit per row (words padded to 256 B).
+// Exit-compaction workspace: the call serial number and an error flag (padded
+// to 256 B), then one 64-bit published count per workgroup of four rows (padded
+// to 256 B).
 extern "C" size_t lsg_workspace_bytes(int op, int64_t B) {
   if ((op != LSG_OP_EXIT_GATE && op != LSG_OP_REL_CHANGE) || B < 0) return 0;
-  const size_t words = (size_t)((B + 31) / 32);
-  return 256 + ((words * 4 + 255) / 256) * 256;
+  const size_t tiles = B > 0 ? (size_t)((B + 3) / 4) : 1;  // an empty batch still launches one workgroup
+  return 256 + ((tiles * 8 + 255) / 256) * 256;
 }

@@ -15,15 +15,11 @@ int32 in ``ModelRunner._sample_logits``, model_runner.py:279-280).
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import TYPE_CHECKING, Any, List
+from typing import Any, List
 
 import torch
 
 from . import _lib
-
-if TYPE_CHECKING:  # pragma: no cover
-    from .core import SamplingParams  # noqa: F401
-
 
 @dataclass
 class BatchSamplingArgs:

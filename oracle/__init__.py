@@ -165,3 +165,87 @@ def bf16_bits(x) -> np.ndarray:
 
     t = x.detach().cpu().contiguous()
     return t.view(torch.int16).numpy().view(np.uint16)
+
+
+class Token:
+    """A decode position in flight: identity (request, slot, position), depth and
+    an optional replay exit depth (CDBDecodeToken, managers/cdb_scheduler.py:39-60)."""
+
+    __slots__ = ("ident", "slot", "depth", "replay", "live")
+
+    def __init__(self, ident, slot: int, depth: int = 0, replay: int | None = None):
+        self.ident, self.slot, self.depth, self.replay, self.live = ident, slot, depth, replay, True
+
+    def advanced(self) -> "Token":
+        t = Token(self.ident, self.slot, self.depth + 1, self.replay)
+        t.live = self.live
+        return t
+
+
+class CdbRouter:
+    """CPU restatement of the CDB scheduler's exit routing for core steps.
+
+    ``core_step`` follows CDBScheduler._run_core (cdb_scheduler.py:232-267):
+    the batch's tokens advance one depth, this step's gate decisions become the
+    current gate, and the previous gate (lookahead timing) or the current one
+    (``disable_lookahead_exit``) is consumed by ``_consume`` (the rules of
+    _consume_gate, cdb_scheduler.py:189-229): replay depths replace decisions
+    (``token.depth >= replay - delay``), a token leaves when
+    ``current.depth >= max_depth or (requested and exit_ready)`` with
+    ``exit_ready = disable_lookahead_exit or current.depth > token.depth``, and
+    the depth cap routes every remaining core token at ``max_depth``.
+    Returns the identities routed to the coda in this step, in routing order.
+    """
+
+    def __init__(self, max_depth: int, disable_lookahead_exit: bool):
+        self.max_depth = max_depth
+        self.direct = disable_lookahead_exit
+        self.core: list[Token] = []
+        self.pending = None
+
+    def add(self, token: Token) -> None:
+        self.core.append(token)
+
+    def cancel(self, ident) -> None:
+        for t in self.core:
+            if t.ident == ident:
+                t.live = False
+        self.core = [t for t in self.core if t.ident != ident]
+
+    def _consume(self, gate) -> list:
+        if gate is None:
+            return []
+        tokens, decisions = gate
+        current = {t.ident: t for t in self.core}
+        decisions = list(decisions)
+        for i, t in enumerate(tokens):
+            if t.replay is not None:
+                decisions[i] = t.depth >= t.replay - (0 if self.direct else 1)
+        exited = []
+        for t, req in zip(tokens, decisions):
+            cur = current.get(t.ident)
+            if cur is None or not cur.live:
+                continue
+            ready = self.direct or cur.depth > t.depth
+            if cur.depth >= self.max_depth or (req and ready):
+                exited.append(cur)
+        ids = {t.ident for t in exited}
+        self.core = [t for t in self.core if t.ident not in ids]
+        return [t.ident for t in exited]
+
+    def core_step(self, batch_idents: list, decisions: list) -> list:
+        """``decisions[i]``: the gate's signal for ``batch_idents[i]`` this step."""
+        advanced = {}
+        for i, t in enumerate(self.core):
+            if t.ident in batch_idents:
+                self.core[i] = advanced[t.ident] = t.advanced()
+        gate_tokens = [advanced[i] for i in batch_idents]
+        current = (gate_tokens, list(decisions))
+        if self.direct:
+            out = self._consume(current)
+        else:
+            previous, self.pending = self.pending, current
+            out = self._consume(previous)
+        capped = [t for t in self.core if t.depth >= self.max_depth]
+        self.core = [t for t in self.core if t.depth < self.max_depth]
+        return out + [t.ident for t in capped]

@@ -321,19 +321,31 @@ void orc_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld,
 /* --------------------------------------------------------------------------
  * Ouro exit gate (G1-G5).
  *   z      = round_dtype( sum_h h[r,h] * w[h] + b )       (layers/linear.py:32-33)
- *   lambda = float32( sigmoid(z) )  evaluated in float64 and rounded once
+ *   lambda = 1 / (1 + exp(-z)) in float32, one rounding per op, exp(-z)
+ *            correctly rounded to float32  (torch's sigmoid(float(z)), exit_gates.py:13)
  *   F'     = F + (1 - F) * lambda  as three float32 ops     (exit_gates.py:13-15)
  *   depth  = loop_step + 1 + lookahead                      (ouro.py:152)
  *   mask   = (F' >= tau) & (depth >= min_loop_steps)        (ouro.py:153-154)
  *            | (max_depth > 0 & loop_step + 1 >= max_depth) (cdb_scheduler.py:221,262-266)
  *   exit_idx / keep_idx: ascending rows with mask 1 / 0    (cdb_scheduler.py:215-228)
- * amb bit 0: the exit decision may differ under fp32 accumulation of z.
+ * amb bit 0: the exit decision may differ from the reference's (bit 2 or bit 3
+ *            changes it).
  * amb bit 2: z itself may round differently under fp32 accumulation.
+ * amb bit 3: |F' - tau| < 1e-6 in the float64 shadow F + (1 - F) * sigmoid(z):
+ *            an exp or sigmoid that differs by an ulp can flip the compare.
  * ------------------------------------------------------------------------ */
-/* lambda = float32(sigmoid(z)) evaluated in float64 and rounded once; then
+/* lambda = 1 / (1 + exp(-z)) in float32 with exp(-z) rounded once from float64
+ * (x86-64 SSE arithmetic: no excess precision), then
  * F' = F + (1 - F) * lambda as three separately rounded float32 ops. */
+static float sigmoid_f32(double z) {
+  volatile float e = (float)exp(-z);
+  volatile float d = 1.0f + e;
+  volatile float lam = 1.0f / d;
+  return lam;
+}
+
 static float gate_update(float F, double z) {
-  float lam = (float)(1.0 / (1.0 + exp(-z)));
+  float lam = sigmoid_f32(z);
   volatile float t1 = 1.0f - F;
   volatile float t2 = t1 * lam;
   volatile float Fn = F + t2;
@@ -346,6 +358,17 @@ static int gate_mask(float Fn, int32_t ls, float tau, int32_t min_loop_steps, in
   int m = (Fn >= tau) && (exit_depth >= min_loop_steps);
   if (max_depth > 0 && ls + 1 >= max_depth) m = 1;
   return m;
+}
+
+/* 1 when the float64 shadow of F' lies within 1e-6 of tau and the compare
+ * decides the mask (depth test passed, no depth cap). */
+static int tau_band(float F, double z, int32_t ls, float tau, int32_t min_loop_steps,
+                    int32_t lookahead, int32_t max_depth) {
+  if (ls + 1 + (lookahead ? 1 : 0) < min_loop_steps) return 0;
+  if (max_depth > 0 && ls + 1 >= max_depth) return 0;
+  double lam = 1.0 / (1.0 + exp(-z));
+  double F64 = (double)F + (1.0 - (double)F) * lam;
+  return fabs(F64 - (double)tau) < 1e-6;
 }
 
 void orc_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh, const void* w,
@@ -383,6 +406,7 @@ void orc_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh, 
         if (mlo != mhi) a |= 1; /* the exit decision itself may differ */
       }
     }
+    if (tau_band(F, z, ls, tau, min_loop_steps, lookahead, max_depth)) a |= 8 | 1;
     if (z_out) z_out[r] = (float)z;
     F_next[r] = Fn;
     mask[r] = (uint8_t)m;

@@ -37,3 +37,23 @@ def dev():
     import torch
 
     return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def SP():
+    """Stand-in for the engine's SamplingParams: the fields Sampler.prepare reads
+    (temperature, top_k, top_p) and ``is_greedy`` as python/loopsgl/core.py:83-85
+    defines it."""
+    from dataclasses import dataclass
+
+    @dataclass
+    class SamplingParams:
+        temperature: float = 0.0
+        top_k: int = -1
+        top_p: float = 1.0
+
+        @property
+        def is_greedy(self) -> bool:
+            return (self.temperature <= 0.0 or self.top_k == 1) and self.top_p == 1.0
+
+    return SamplingParams

@@ -245,12 +245,11 @@ def test_graph_replay(lsg, dev):
     assert torch.equal(out, lsg.sample_rows(*args))
 
 
-def test_sampler_prepare_and_sample(lsg, orc, dev):
+def test_sampler_prepare_and_sample(lsg, orc, dev, SP):
     """Sampler.prepare normalises per-request params; sample draws with the
     given uniforms (greedy rows in a mixed batch use T=1e-6)."""
     from types import SimpleNamespace
 
-    SP = lsg.SamplingParams
     reqs = [SimpleNamespace(sampling_params=p) for p in
             [SP(), SP(temperature=0.8, top_k=20), SP(temperature=1.0, top_p=0.9), SP(top_k=1, temperature=2.0)]]
     s = lsg.Sampler(dev, 3000)

@@ -12,36 +12,6 @@ import torch
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-# ------------------------------------------------------- SamplingParams -------
-def test_sampling_params_verify(lsg):
-    """core.py:54-81: invalid values raise ValueError."""
-    SP = lsg.SamplingParams
-    SP().verify()
-    SP(temperature=0.7, top_k=50, top_p=0.9).verify()
-    for bad in (dict(temperature=-1.0), dict(temperature=float("inf")), dict(temperature=True),
-                dict(top_p=0.0), dict(top_p=1.5), dict(top_p=float("nan")), dict(top_k=0),
-                dict(top_k=-2), dict(top_k=2.0), dict(max_tokens=0)):
-        with pytest.raises(ValueError):
-            SP(**bad).verify()
-
-
-def test_is_greedy(lsg):
-    """core.py:83-85: greedy iff (T <= 0 or k == 1) and p == 1."""
-    SP = lsg.SamplingParams
-    assert SP().is_greedy
-    assert SP(temperature=0.8, top_k=1).is_greedy
-    assert not SP(temperature=0.8).is_greedy
-    assert not SP(temperature=0.0, top_p=0.9).is_greedy
-    assert not SP(top_k=1, top_p=0.5).is_greedy
-
-
-def test_loop_params(lsg):
-    lsg.LoopParams(loop_steps=4, exit_threshold=0.2)
-    for bad in (0, -1, True, 2.0):
-        with pytest.raises(ValueError):
-            lsg.LoopParams(loop_steps=bad)
-
-
 # -------------------------------------------------------- Sampler.prepare ----
 def _prepare(lsg, monkeypatch, params, vocab=100):
     import loop_sglang_amd.sampler as sampler_mod
@@ -52,17 +22,15 @@ def _prepare(lsg, monkeypatch, params, vocab=100):
     return s.prepare(SimpleNamespace(reqs=[SimpleNamespace(sampling_params=p) for p in params]))
 
 
-def test_prepare_all_greedy(lsg, monkeypatch):
-    SP = lsg.SamplingParams
+def test_prepare_all_greedy(lsg, monkeypatch, SP):
     args = _prepare(lsg, monkeypatch, [SP(), SP(temperature=0.5, top_k=1)])
     assert args.temperatures is None and args.top_k is not None and args.top_p is None
     assert args.top_k.tolist() == [100, 1]
 
 
-def test_prepare_mixed(lsg, monkeypatch):
+def test_prepare_mixed(lsg, monkeypatch, SP):
     """sample.py:89-105: greedy rows get T = 1e-6 once any row samples; k < 1
     becomes V; tensors are None when neutral for every row."""
-    SP = lsg.SamplingParams
     args = _prepare(lsg, monkeypatch, [SP(), SP(temperature=0.8), SP(temperature=1.2, top_p=0.9),
                                        SP(temperature=0.5, top_k=7)])
     assert torch.allclose(args.temperatures, torch.tensor([1e-6, 0.8, 1.2, 0.5]))
@@ -144,8 +112,9 @@ def test_capi_argument_errors_without_gpu(lsg):
     rc = L.lsg_sample(ctypes.c_void_p(16), 9, 4, 10, 10, None, None, None, None, None, 4, None,
                       ctypes.c_void_p(16), None)
     assert rc == 1 and b"dtype" in L.lsg_last_error()
-    assert L.lsg_workspace_bytes(1, 512) == 512
-    assert L.lsg_workspace_bytes(1, 100000) == 256 + ((100000 + 31) // 32 * 4 + 255) // 256 * 256
+    # serial number page + one 64-bit word per four rows, padded to 256 B
+    assert L.lsg_workspace_bytes(1, 512) == 256 + 1024
+    assert L.lsg_workspace_bytes(1, 100000) == 256 + ((100000 + 3) // 4 * 8 + 255) // 256 * 256
     assert L.lsg_workspace_bytes(7, 10) == 0
     rc = L.lsg_exit_gate(ctypes.c_void_p(16), 1, 8, 16, 16, ctypes.c_void_p(16), None, None,
                          ctypes.c_void_p(16), None, None, 0, 0.5, 1, 0, 0, ctypes.c_void_p(16),
@@ -154,3 +123,12 @@ def test_capi_argument_errors_without_gpu(lsg):
     rc = L.lsg_exit_gate(None, 1, 8, 16, 16, None, None, None, None, None, None, 0, 0.5, 1, 0, 0,
                          None, None, None, None, None, None, 0, None)
     assert rc == 1
+    # lookahead routing needs the pending-gate pool, then a workspace
+    rc = L.lsg_exit_gate_route(ctypes.c_void_p(16), 1, 8, 16, 16, ctypes.c_void_p(16), None, None,
+                               ctypes.c_void_p(16), None, None, 0, 0.5, 1, 0, 0, 0, None, None,
+                               ctypes.c_void_p(16), None, None, None, None, None, None, 0, None)
+    assert rc == 1 and b"pending" in L.lsg_last_error()
+    rc = L.lsg_exit_gate_route(ctypes.c_void_p(16), 1, 8, 16, 16, ctypes.c_void_p(16), None, None,
+                               ctypes.c_void_p(16), None, None, 0, 0.5, 1, 0, 0, 0, ctypes.c_void_p(16),
+                               None, ctypes.c_void_p(16), None, None, None, None, None, None, 0, None)
+    assert rc == 3 and b"workspace" in L.lsg_last_error()

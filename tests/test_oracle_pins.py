@@ -227,7 +227,130 @@ def test_gate_product_form_and_expit(orc):
         surv *= 1 - expit(z[t].astype(np.float64))
         np.testing.assert_allclose(F, 1 - surv, atol=2e-6)
     lam = orc.cumulative_exit_probability(z[0], np.zeros(1000, np.float32))
-    np.testing.assert_array_equal(lam, expit(z[0].astype(np.float64)).astype(np.float32))
+    want = expit(z[0].astype(np.float64)).astype(np.float32)
+    # float32 evaluation of 1 / (1 + exp(-z)) (three roundings): within two ulps
+    # of the rounded exact value
+    assert np.abs(lam.view(np.int32) - want.view(np.int32)).max() <= 2
+
+
+def _finite_half_values():
+    """Every finite bf16 and fp16 value, as float32 (the gate logit's dtypes)."""
+    bits = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16)
+    out = []
+    for dt in (torch.bfloat16, torch.float16):
+        z = bits.view(dt).float()
+        out.append(z[torch.isfinite(z)])
+    return torch.cat(out).numpy()
+
+
+def test_sigmoid_is_float32_formula(orc):
+    """G2: for every finite bf16 and fp16 z, lambda is exactly
+    float32(1 / float32(1 + e)) with e = exp(-z) correctly rounded to float32 --
+    the float32 formula torch's sigmoid evaluates -- where e comes from a
+    40-digit decimal exp and the + and / are numpy's IEEE float32 operations."""
+    from decimal import Context, Decimal
+
+    z = _finite_half_values()
+    ctx = Context(prec=40)
+
+    def exp_neg(v):
+        x = -float(v)
+        return float("inf") if x > 200 else 0.0 if x < -200 else float(ctx.exp(Decimal(x)))
+
+    with np.errstate(over="ignore"):
+        e = np.array([exp_neg(v) for v in z]).astype(np.float32)
+        want = np.float32(1) / (np.float32(1) + e)
+    lam = orc.cumulative_exit_probability(z, np.zeros(z.size, np.float32))
+    assert np.array_equal(lam.view(np.int32), want.astype(np.float32).view(np.int32))
+
+
+def test_sigmoid_matches_torch_float32(orc):
+    """G2/G4 against torch's own CPU float32 sigmoid (exit_gates.py:13) over every
+    finite bf16 and fp16 z: lambda within two ulps (torch's vectorised CPU exp is
+    not correctly rounded); F' against ``prev + (1 - prev) * z.float().sigmoid()``;
+    every row whose mask flips between the two at a threshold lies inside the
+    flagged tau band."""
+    z = _finite_half_values()
+    lam = orc.cumulative_exit_probability(z, np.zeros(z.size, np.float32))
+    lam_t = torch.sigmoid(torch.from_numpy(z)).numpy()
+    ulp = np.abs(lam.view(np.int32).astype(np.int64) - lam_t.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2
+    assert (ulp == 0).mean() > 0.99
+    rng = np.random.default_rng(5)
+    F = rng.random(z.size).astype(np.float32) * 0.9
+    Fn = orc.cumulative_exit_probability(z, F)
+    Ft = torch.from_numpy(F)
+    Fn_t = (Ft + (1.0 - Ft) * torch.sigmoid(torch.from_numpy(z))).numpy()
+    assert np.abs(Fn.astype(np.float64) - Fn_t).max() < 4e-7
+    # identity gate (H = 1, w = 1, no bias) so z = h exactly; thresholds at the
+    # values where the two F' disagree most often
+    diff = np.nonzero(Fn != Fn_t)[0]
+    assert diff.size > 0
+    h = torch.from_numpy(z[diff]).to(torch.float32).numpy().reshape(-1, 1)
+    for tau in np.unique(np.concatenate([Fn[diff][:50], Fn_t[diff][:50]])):
+        r = orc.exit_gate(h, np.ones(1, np.float32), None, F[diff], 0, float(tau), dtype=orc.F32)
+        ref = Fn_t[diff] >= np.float32(tau)
+        flip = r["mask"].astype(bool) != ref
+        assert ((r["amb"][flip] & 9) == 9).all()
+
+
+def test_exp_rounding_is_safe(orc):
+    """exp(-z) rounded from float64 to float32 is the correctly rounded float32
+    exp for every finite bf16 and fp16 z, whichever float64 exp computes it
+    (device or host) as long as its error stays under two float64 ulps: the
+    exact value lies at least four float64 ulps away from every float32
+    rounding boundary (the closest case is z = 2^-25, where exp(-z) sits
+    z^2/2 above the midpoint 1 - 2^-25)."""
+    z = _finite_half_values().astype(np.float64)
+    with np.errstate(over="ignore"):
+        e = np.exp(-z)
+    ok = np.isfinite(e) & (e >= np.float64(np.finfo(np.float32).tiny))
+    ok &= e < np.float64(np.finfo(np.float32).max)
+    e = e[ok]
+    f = e.astype(np.float32)
+    lo = np.nextafter(f, np.float32(0)).astype(np.float64)
+    hi = np.nextafter(f, np.float32(np.inf)).astype(np.float64)
+    fd = f.astype(np.float64)
+    gap = np.minimum(np.abs(e - (fd + lo) / 2), np.abs(e - (fd + hi) / 2))
+    assert (gap / np.spacing(e)).min() >= 4
+
+
+def test_router_reference_kat(orc):
+    """tests/core/test_scheduler.py:65-78: a depth-two replay exits at depth two
+    under either gate timing; a replacement request in the same slot is not
+    routed by the old token's gate."""
+    for direct in (False, True):
+        r = orc.CdbRouter(max_depth=4, disable_lookahead_exit=direct)
+        r.add(orc.Token(("req0", 0, 2), 0, depth=2, replay=2))
+        gate_token = orc.Token(("req0", 0, 2), 0, depth=2 if direct else 1, replay=2)
+        assert r._consume(([gate_token], [False])) == [("req0", 0, 2)]
+        r = orc.CdbRouter(max_depth=4, disable_lookahead_exit=direct)
+        r.add(orc.Token(("req0b", 0, 2), 0, depth=1))
+        assert r._consume(([gate_token], [False])) == []
+        assert len(r.core) == 1
+
+
+def test_router_timings(orc):
+    """The same replay and request sequence under both timings: direct routing
+    exits in the step the gate fires; lookahead routing one core step later
+    (the token advanced once more), and a gate whose token skipped the next core
+    step is dropped; the depth cap routes at max_depth either way."""
+    for direct in (False, True):
+        r = orc.CdbRouter(max_depth=4, disable_lookahead_exit=direct)
+        r.add(orc.Token("a", 0))
+        r.add(orc.Token("b", 1, replay=2))
+        r.add(orc.Token("c", 2))
+        s1 = r.core_step(["a", "b", "c"], [True, False, False])
+        assert s1 == (["a"] if direct else [])
+        s2 = r.core_step(["b", "c"] if direct else ["a", "b", "c"], [False, False, True])
+        assert s2 == (["b"] if direct else ["a", "b"])
+        # c requested at its second step; under lookahead it skips the next step
+        s3 = r.core_step([] if not direct else ["c"], [] if not direct else [False])
+        assert s3 == ([] if not direct else [])
+        s4 = r.core_step(["c"], [False])
+        assert s4 == ([] if not direct else ["c"])
+        if not direct:
+            assert r.core_step(["c"], [False]) == ["c"]  # depth cap at 4
 
 
 def test_gate_dot_and_compaction(orc):
