@@ -106,6 +106,24 @@ int lsg_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh, c
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * lsg_exit_gate for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has
+ * no counterpart in the reference.  Same arguments and results as lsg_exit_gate
+ * without the workspace: the compaction uses a static device array inside the
+ * library (one per GPU, about 128 KiB, held until the process ends), looked up
+ * for the current device, which must be the stream's device.
+ *   B             at most 65536 rows (LSG_ERR_ARG beyond).
+ * Calls that overlap in time on one GPU share that array and race: serialise
+ * them (one stream, or events).  Nothing is allocated or freed.
+ */
+int lsg_exit_gate_noalloc(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh,
+                          const void* w, const void* bias, const float* F_prev, float* F_next,
+                          const int32_t* slots, const int32_t* loop_step, int32_t loop_step_scalar,
+                          float tau, int32_t min_loop_steps, int32_t lookahead, int32_t max_depth,
+                          uint8_t* mask, int32_t* exit_idx, int32_t* keep_idx, int32_t* n_exit,
+                          float* z_out, void* stream);
+
+/*
  * One core step of the Ouro gate with the scheduler's exit routing.  Replaces,
  * besides what lsg_exit_gate replaces, the routing rules of CDBScheduler.
  * _consume_gate and _run_core (managers/cdb_scheduler.py:207-222,254-266).

@@ -25,6 +25,8 @@ SIGNATURES = {
     "lsg_sample": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _P]),
     "lsg_exit_gate": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _F,
                                      _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "lsg_exit_gate_noalloc": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P,
+                                             _I32, _F, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
     "lsg_exit_gate_route": (ctypes.c_int, [_P, ctypes.c_int, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32,
                                            _F, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                            _SZ, _P]),

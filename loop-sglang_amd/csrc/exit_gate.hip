@@ -22,6 +22,8 @@
 // Compiled with -ffp-contract=off: lambda = 1 / (1 + exp(-z)) and
 // F' = F + (1 - F) * lambda are separately rounded fp32 operations, as torch
 // evaluates them (one rounding per op).
+#include <mutex>
+
 #include "lsg_capi_internal.h"
 #include "lsg_common.h"
 
@@ -427,9 +429,61 @@ static int gate_common(const char* fn, const void* h, int dtype, int64_t B, int6
   return check_launch(fn);
 }
 
+// Workspace of lsg_exit_gate_noalloc: a file-scope device array, one copy per
+// GPU, zero at load and never cleared afterwards (the call serial number kept in
+// it tells each call's published words from older ones).  Its host-side name is
+// not a device address: kernels get the address hipGetSymbolAddress returns for
+// the current device, looked up once per device.
+constexpr int64_t kNoAllocMaxRows = 65536;
+constexpr size_t kScratchBytes = 256 + (size_t)(kNoAllocMaxRows / kGateRows) * 8;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_for_current_device(void** out, const char* fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(LSG_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(LSG_ERR_ARG, "%s: device %d out of range", fn, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(LSG_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LSG_OK;
+}
+
 }  // namespace lsg
 
 using namespace lsg;
+
+extern "C" int lsg_exit_gate_noalloc(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh,
+                                     const void* w, const void* bias, const float* F_prev,
+                                     float* F_next, const int32_t* slots,
+                                     const int32_t* loop_step, int32_t loop_step_scalar, float tau,
+                                     int32_t min_loop_steps, int32_t lookahead, int32_t max_depth,
+                                     uint8_t* mask, int32_t* exit_idx, int32_t* keep_idx,
+                                     int32_t* n_exit, float* z_out, void* stream) {
+  clear_error();
+  if (B > kNoAllocMaxRows)
+    return set_error(LSG_ERR_ARG, "lsg_exit_gate_noalloc: B=%lld exceeds the static workspace's %lld rows",
+                     (long long)B, (long long)kNoAllocMaxRows);
+  void* ws = nullptr;
+  if (exit_idx || keep_idx || n_exit) {
+    const int rc = scratch_for_current_device(&ws, "lsg_exit_gate_noalloc");
+    if (rc != LSG_OK) return rc;
+  }
+  return gate_common("lsg_exit_gate_noalloc", h, dtype, B, H, ldh, w, bias, F_prev, F_next, slots,
+                     loop_step, loop_step_scalar, tau, min_loop_steps, lookahead, max_depth, 1, 1,
+                     nullptr, nullptr, mask, nullptr, exit_idx, keep_idx, n_exit, z_out, ws,
+                     ws ? kScratchBytes : 0, stream);
+}
 
 extern "C" int lsg_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh,
                              const void* w, const void* bias, const float* F_prev, float* F_next,
