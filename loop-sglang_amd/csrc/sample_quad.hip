@@ -49,6 +49,8 @@ constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order ov
 constexpr int kSeg = 128;         // window entries staged per wave
 constexpr int kWin = 256;         // window finished by one wave (4 entries per lane)
 constexpr int kRB = 256;          // refinement bins per level
+constexpr int kVB = 512;          // value bins bracketing an exact top-p threshold
+constexpr int kCW = 384;          // bracket candidates per wave
 constexpr double kFix = 1099511627776.0;  // 2^40
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kNonTemporal = 2;   // buffer-load cache policy: stream through the caches
@@ -144,6 +146,16 @@ struct Smem {
     struct {                                      // exact refinement and its inverse CDF
       unsigned long long rb[4][kRB + 1];          // refinement bins, four copies by lane
       double colsum[kNW][CAP];                    // kept mass per wave and chunk column
+    };
+    struct {                                      // exact top-p, pass 1
+      uint32_t vh[kNW][kVB + 1];                  // value histograms per wave (bin kVB: sink), 2^-16 of the bin top
+    };
+    struct {                                      // exact top-p, pass 2 and the threshold
+      uint32_t ckey[kNW][kCW];                    // bracket candidates per wave: order key >> SH,
+      float cmass[kNW][kCW];                      //   mass,
+      uint32_t cpos[kNW][kCW];                    //   (column * 64 + lane) * 8 + element
+      double kbin[kRB];                           // key bins (masses)
+      double ksum[kNW][CAP];                      // kept mass per wave and chunk column
     };
   };
   float wmax[kNW];
@@ -546,6 +558,10 @@ __device__ __forceinline__ bool refine(const Row<T, CAP>& R, Smem<CAP>& S, float
   return false;
 }
 
+template <typename T, int CAP>
+__device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP>& S, const double (*colsum)[CAP], float m,
+                                          float c, float thr, float u, int32_t* out);
+
 // Fallback for top-k / top-p rows without a usable window: exact refinement,
 // then the inverse CDF over {x >= thr} with fresh masses.  Every wave calls.
 template <typename T, int CAP>
@@ -588,7 +604,17 @@ __device__ __forceinline__ void row_exact(const Row<T, CAP>& R, Smem<CAP>& S, fl
   });
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
-  const double cs = lane < CAP ? S.colsum[wid][lane] : 0.0;
+  kept_draw(R, S, S.colsum, m, c, thr, u, out);
+}
+
+// Inverse CDF over the kept elements {x >= thr} given their mass per wave and
+// chunk column (this wave's row of colsum complete and visible to it).
+template <typename T, int CAP>
+__device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP>& S, const double (*colsum)[CAP], float m,
+                                          float c, float thr, float u, int32_t* out) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  auto emass = [&](float x) { return x >= thr ? ex2c((x - m) * c) : 0.0f; };
+  const double cs = lane < CAP ? colsum[wid][lane] : 0.0;
   const double cinc = wave_incl_scan(cs, lane);
   if (lane == 63) S.wz[wid] = cinc;
   __syncthreads();
@@ -604,6 +630,196 @@ __device__ __forceinline__ void row_exact(const Row<T, CAP>& R, Smem<CAP>& S, fl
   }
   const double colex = readlane_d(cinc - cs, js);
   finish_column<T, CAP>(R.load(js), ws, js, colex, Uw, emass, out);
+}
+
+// Exact top-p (no top-k) for rows without a usable window, in two passes over
+// the row.  The threshold's value y* = (x* - m) c lies above
+// ylo = log2((1 - p) Z / V): the elements below ylo weigh less than (1 - p) Z
+// together.  Pass 1 builds kVB equal-width value bins over [ylo, 0], each
+// holding its members' masses relative to the bin top in 2^-16 fixed point
+// (integer sums, at most 2^-15 low relative to the exact bin mass); the
+// cumulative from the top then brackets y* between bins b1 (cumulative
+// >= p Z (1 - 2^-14)) and b2 (>= p Z (1 + 2^-20)): bins above b1 are kept,
+// bins below b2 dropped, whatever the rounding.  Pass 2 sums the kept mass per
+// chunk column and lists the bracket's elements (key, mass, position) in LDS,
+// where key bins settle the exact threshold key; the kept candidates' masses
+// then join their columns and the inverse CDF runs as in row_exact.  Returns
+// false (uniformly, having written nothing) when the bracket cannot be formed
+// or its candidates overflow kCW per wave.  Every wave calls.
+template <typename T, int CAP>
+__device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S, float m, float c, double Z, float p,
+                                              float Lm, float u, int64_t V, int32_t* out) {
+  constexpr int EPV = QE<T>::EPV, SH = QE<T>::SH;
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const double target = (double)p * Z;
+  float ylo = log2f((float)((1.0 - (double)p) * Z / (double)V)) - 0.01f;
+  ylo = fmaxf(ylo, fmaxf(Lm, -40.0f));
+  if (!(ylo < -0x1p-10f)) return false;
+  const float s = (float)kVB / -ylo, w = -ylo / (float)kVB;
+  auto vbin = [&](float y) { return min(kVB - 1, (int)(-y * s)); };
+  // pass 1: value histograms
+  for (int i = t; i < kNW * (kVB + 1); i += kNT) (&S.vh[0][0])[i] = 0u;
+  __syncthreads();
+  {
+    uint32_t* vh = S.vh[wid];
+    each_chunk_mem(R, S, [&](float cb) { return (cb - m) * c >= ylo; }, [&](int, const v4u& v, bool may) {
+      float x[EPV];
+      QE<T>::unpack(v, x);
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        const float y = (x[i] - m) * c;
+        const int b = vbin(y);
+        const bool ok = may && y >= ylo;
+        const float er = ex2c(y + (float)b * w);
+        atomicAdd(&vh[ok ? b : kVB], (uint32_t)(er * 65536.0f));
+      }
+    });
+  }
+  __syncthreads();
+  // bracket (every wave alike): lane l holds bins 8l .. 8l+7
+  int b1 = -1, b2 = -1;
+  {
+    double bm[8], ls = 0.0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int b = 8 * lane + q;
+      const uint64_t hsum = (uint64_t)S.vh[0][b] + S.vh[1][b] + S.vh[2][b] + S.vh[3][b];
+      bm[q] = (double)hsum * (double)__builtin_amdgcn_exp2f(-((float)b * w)) * 0x1p-16;
+      ls += bm[q];
+    }
+    const double incl = wave_incl_scan(ls, lane);
+    const double t1 = target * (1.0 - 0x1p-14), t2 = target * (1.0 + 0x1p-20);
+    const uint64_t bal1 = __ballot(incl >= t1), bal2 = __ballot(incl >= t2);
+    if (bal1 && bal2) {
+      const int l1 = __ffsll((unsigned long long)bal1) - 1, l2 = __ffsll((unsigned long long)bal2) - 1;
+      double a1 = readlane_d(incl - ls, l1), a2 = readlane_d(incl - ls, l2);
+      b1 = 8 * l1 + 7;
+      b2 = 8 * l2 + 7;
+#pragma unroll
+      for (int q = 7; q >= 0; --q) {  // first bin of the lane reaching each target
+        const double v1 = readlane_d(bm[q], l1), v2 = readlane_d(bm[q], l2);
+        double c1 = a1, c2 = a2;
+#pragma unroll
+        for (int r = 0; r < q; ++r) {
+          c1 += readlane_d(bm[r], l1);
+          c2 += readlane_d(bm[r], l2);
+        }
+        if (c1 + v1 >= t1) b1 = 8 * l1 + q;
+        if (c2 + v2 >= t2) b2 = 8 * l2 + q;
+      }
+    }
+  }
+  __syncthreads();  // every wave has read the histograms
+  if (b1 < 0 || b2 < 0) return false;
+  // pass 2: kept mass per column (bins above b1), candidates (bins b1 .. b2)
+  int nc = 0;
+  if (lane < CAP) S.ksum[wid][lane] = 0.0;
+  each_chunk_mem(R, S, [&](float cb) { return (cb - m) * c >= ylo; }, [&](int j, const v4u& v, bool may) {
+    float x[EPV], e[EPV];
+    QE<T>::unpack(v, x);
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      const float y = (x[i] - m) * c;
+      const int b = vbin(y);
+      const bool ok = may && y >= ylo;
+      const float ei = ex2c(y);
+      e[i] = ok && b < b1 ? ei : 0.0f;
+      const bool cd = ok && b >= b1 && b <= b2;
+      const uint64_t bal = __ballot(cd);
+      if (bal) {
+        const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (cd && pos < kCW) {
+          S.ckey[wid][pos] = okey(x[i]) >> SH;
+          S.cmass[wid][pos] = ei;
+          S.cpos[wid][pos] = ((uint32_t)(j * kWave + lane) << 3) | (uint32_t)i;
+        }
+        nc += (int)__popcll(bal);
+      }
+    }
+    const double C = wave_sum((double)tree_sum(e));
+    if (lane == 0) S.ksum[wid][j] = C;
+  });
+  if (lane == 0) S.cnt[wid] = nc;
+  __syncthreads();
+  int cq[kNW];
+  bool ovf = false;
+#pragma unroll
+  for (int q = 0; q < kNW; ++q) {
+    cq[q] = uni(S.cnt[q]);
+    ovf = ovf || cq[q] > kCW;
+  }
+  if (ovf) return false;
+  // mass above the bracket: every kept column sum so far
+  double above = 0.0;
+#pragma unroll
+  for (int q = 0; q < kNW; ++q) {
+    const double cs = lane < CAP ? S.ksum[q][lane] : 0.0;
+    above += wave_sum(cs);
+  }
+  // key bracket of bins b1 .. b2: their y range widened by half a bin, mapped
+  // back to x, then a few more keys for the rounding of that mapping
+  constexpr uint32_t kSlack = SH ? 2u : 64u;
+  uint32_t hi = (okey(fminf(m, m + (-(float)b1 * w + 0.5f * w) / c)) >> SH) + 1u + kSlack;
+  hi = min(hi, (okey(m) >> SH) + 1u);
+  const uint32_t kb = okey(m + (-(float)(b2 + 1) * w - 0.5f * w) / c) >> SH;
+  uint32_t lo = kb > kSlack ? kb - kSlack : 0u;
+  uint32_t thr_key = 0u;
+  bool found = false;
+  for (int level = 0; level < 6 && !found; ++level) {
+    if (hi <= lo) return false;
+    int sh = 0;
+    while (((hi - lo - 1u) >> sh) >= (uint32_t)kRB) ++sh;
+    if (t < kRB) S.kbin[t] = 0.0;
+    __syncthreads();
+    for (int q = t; q < kNW * kCW; q += kNT) {
+      const int cw = q / kCW, ci = q - cw * kCW;
+      if (ci < cq[cw]) {
+        const uint32_t key = S.ckey[cw][ci];
+        if (key >= lo && key < hi) atomicAdd(&S.kbin[(hi - 1u - key) >> sh], (double)S.cmass[cw][ci]);
+      }
+    }
+    __syncthreads();
+    double bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = S.kbin[4 * lane + q];
+    const double ls = (bv[0] + bv[1]) + (bv[2] + bv[3]);
+    const double incl = wave_incl_scan(ls, lane);
+    const uint64_t bal = __ballot(above + incl >= target);
+    __syncthreads();  // every wave has read the bins
+    if (!bal) return false;
+    const int lb = __ffsll((unsigned long long)bal) - 1;
+    double a = above + readlane_d(incl - ls, lb);
+    int bs = 4 * lb + 3;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const double vq = readlane_d(bv[q], lb);
+      if (a + vq >= target) {
+        bs = 4 * lb + q;
+        break;
+      }
+      a += vq;
+    }
+    above = a;
+    const uint32_t nhi = hi - ((uint32_t)bs << sh);
+    const uint32_t nlo = nhi - lo > (1u << sh) ? nhi - (1u << sh) : lo;
+    lo = nlo;
+    hi = nhi;
+    if (hi - lo == 1u) {
+      thr_key = lo;
+      found = true;
+    }
+  }
+  if (!found) return false;
+  // the kept candidates join their columns
+  for (int q = t; q < kNW * kCW; q += kNT) {
+    const int cw = q / kCW, ci = q - cw * kCW;
+    if (ci < cq[cw] && S.ckey[cw][ci] >= thr_key)
+      atomicAdd(&S.ksum[cw][(S.cpos[cw][ci] >> 3) / kWave], (double)S.cmass[cw][ci]);
+  }
+  __syncthreads();
+  kept_draw(R, S, S.ksum, m, c, key_value(thr_key << SH), u, out);
+  return true;
 }
 
 // Entry ranked r-th largest (1-based) among the window entries of one fine bin
@@ -1048,7 +1264,9 @@ void quad_sample_kernel(SampleParams P) {
   }
   double Zq[kNW];
   wave_masses(S, m, c, Zq);
-  row_exact(R, S, m, c, ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3], kon, k, pon, p, bstar >= 0 ? Lm : -INFINITY, u, out);
+  const double Zr = ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3];
+  if (!kon && row_topp_fast(R, S, m, c, Zr, p, bstar >= 0 ? Lm : -INFINITY, u, P.V, out)) return;
+  row_exact(R, S, m, c, Zr, kon, k, pon, p, bstar >= 0 ? Lm : -INFINITY, u, out);
 }
 
 // All-greedy batch: torch.argmax per row.
