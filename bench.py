@@ -7,7 +7,10 @@ is one lsg_sample launch over one batch.  Inputs are resident in HBM before the
 timed region; the timed region replays a HIP graph of K launches that rotate
 over NBUF distinct logits buffers (> 512 MB in total, so the 256 MB Infinity
 Cache cannot serve them), bracketed by torch.cuda.synchronize() and timed with
-HIP events on the launch stream.
+HIP events on the launch stream; the graph is replayed five times, each replay
+timed on its own, and the median replay gives ms_per_step ("timing" holds the
+spread).  cpu_baseline times the same step restated in torch on the host CPU,
+at all host threads and at one.
 
 Prints one JSON line (metric / value / roofline / cpu_baseline ...).
 
@@ -117,8 +120,13 @@ def _traffic_from_profiles(workload: str):
         return None
 
 
+REPLAYS = 5
+
+
 def _time_graph(torch, launch, nlaunch: int, warmup: int):
-    """Warm up eagerly, capture nlaunch launches in one graph, time one replay."""
+    """Warm up eagerly, capture nlaunch launches in one graph, then time REPLAYS
+    replays one by one (HIP events on the current stream, where the replay is
+    launched, synchronised on both sides).  Returns the seconds of every timed replay."""
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
@@ -131,31 +139,127 @@ def _time_graph(torch, launch, nlaunch: int, warmup: int):
     torch.cuda.synchronize()
     graph.replay()  # untimed replay: graph upload
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / 1e3  # seconds
+    times = []
+    for _ in range(REPLAYS):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()  # graph.replay() launches on the current stream
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / 1e3)
+    return times
 
 
-def _cpu_baseline_sampling(wl, rows: int):
-    import numpy as np
+def _median(v):
+    v = sorted(v)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
 
-    import oracle
 
+def _timing(times, K):
+    return {"replays": len(times), "steps_per_replay": K,
+            "ms_per_step_median": _median(times) / K * 1e3,
+            "ms_per_step_min": min(times) / K * 1e3, "ms_per_step_max": max(times) / K * 1e3}
+
+
+def _host_threads():
+    """Host threads for the all-cores CPU baseline: the affinity mask, capped by
+    OMP_NUM_THREADS when the environment sets it (a shared host's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return n
+
+
+def _timed_threads(torch, fn, min_seconds: float):
+    """Calls fn() until min_seconds have passed; returns calls per second."""
+    fn()  # warm-up (allocations, thread pool)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            return n / dt
+
+
+def _torch_cpu_sampling(torch, x, T, K, P, U):
+    """The reference's token step restated in torch on the CPU: argmax for an
+    all-greedy batch (sample.py:110-111), else softmax(x / T) (sample.py:66-68),
+    top-k then top-p filtering on the descending sort (sample.py:72-81: kept set
+    = the largest k, then the smallest prefix holding p of the renormalised
+    mass, ties at the threshold kept) and the inverse CDF in vocabulary order
+    with one uniform per row."""
+    if T is None:
+        return torch.argmax(x, dim=-1).to(torch.int32)
+    xf = x.float()
+    probs = torch.softmax(xf / T[:, None], dim=-1)
+    V = x.shape[1]
+    if K is not None:
+        kk = torch.where((K >= 1) & (K < V), K, torch.full_like(K, V)).long()
+        kth = torch.topk(probs, int(kk.max()), dim=-1).values.gather(1, (kk - 1)[:, None])
+        probs = torch.where(probs >= kth, probs, torch.zeros_like(probs))  # ties at the k-th kept
+    thr = torch.zeros_like(probs[:, :1])
+    if P is not None:
+        srt, _ = torch.sort(probs, dim=-1, descending=True)
+        cs = torch.cumsum(srt, dim=-1)
+        idx = torch.searchsorted(cs, P[:, None] * cs[:, -1:]).clamp_max(V - 1)
+        thr = srt.gather(1, idx)  # the smallest kept value; its ties are kept too
+    kept = torch.where((probs >= thr) & (probs > 0), probs, torch.zeros_like(probs))
+    cdf = torch.cumsum(kept, dim=-1)
+    ids = torch.searchsorted(cdf, (U * cdf[:, -1])[:, None], right=True).clamp_max(V - 1)
+    return ids[:, 0].to(torch.int32)
+
+
+def _cpu_baseline_sampling(torch, wl, rows: int, seconds: float):
+    """torch-CPU restatement of the sampling step on a bounded sample of the
+    workload's rows, at all host threads and at one."""
     x = wl["logits"][:rows].cpu()
-    arr = x.numpy() if x.dtype.itemsize == 4 else oracle.bf16_bits(x)
-    code = oracle.F32 if x.dtype.itemsize == 4 else oracle.BF16
-    sel = lambda t: None if t is None else t[:rows].cpu().numpy()
-    threads = 1
-    t0 = time.perf_counter()
-    oracle.sample(arr, sel(wl["temperatures"]), sel(wl.get("top_k")), sel(wl["top_p"]), sel(wl["uniforms"]),
-                  dtype=code, nthreads=threads)
-    dt = time.perf_counter() - t0
-    del np
-    return rows / dt, threads
+    sel = lambda t: None if t is None else t[:rows].cpu()
+    args = (x, sel(wl["temperatures"]), sel(wl.get("top_k")), sel(wl["top_p"]), sel(wl["uniforms"]))
+    prev = torch.get_num_threads()
+    out = {}
+    try:
+        for n in (_host_threads(), 1):
+            torch.set_num_threads(n)
+            out[n] = rows * _timed_threads(torch, lambda: _torch_cpu_sampling(torch, *args), seconds)
+    finally:
+        torch.set_num_threads(prev)
+    return out
+
+
+def _torch_cpu_gate(torch, h, w, b, F, step, tau):
+    """The reference's gate step restated in torch on the CPU: F.linear in the
+    model dtype (ouro.py:149, linear.py:32-33), F' = F + (1 - F) sigmoid(z)
+    (exit_gates.py:13-15), the threshold and depth test (ouro.py:151-154) and
+    the stable exit/keep filter (cdb_scheduler.py:215-228)."""
+    z = torch.nn.functional.linear(h, w[None, :], b).squeeze(-1)
+    Fn = F + (1.0 - F) * z.float().sigmoid()
+    mask = (Fn >= tau) & (step + 1 >= 1)
+    return Fn, torch.nonzero(mask)[:, 0].to(torch.int32), torch.nonzero(~mask)[:, 0].to(torch.int32)
+
+
+def _cpu_baseline_gate(torch, wl, seconds: float):
+    h = [t.cpu() for t in wl["hidden"]]
+    w, b = wl["weight"].cpu(), wl["bias"].cpu()
+    F0 = torch.zeros(h[0].shape[0])
+    prev = torch.get_num_threads()
+    out = {}
+
+    def four_steps():
+        F = F0
+        for st, hs in enumerate(h):
+            F, _, _ = _torch_cpu_gate(torch, hs, w, b, F, st, wl["tau"])
+
+    try:
+        for n in (_host_threads(), 1):
+            torch.set_num_threads(n)
+            out[n] = len(h) * _timed_threads(torch, four_steps, seconds)
+    finally:
+        torch.set_num_threads(prev)
+    return out
 
 
 def _probe(torch, launch, dev):
@@ -215,17 +319,22 @@ def main():
         if a.traffic_probe:
             _probe(torch, launch, dev)
             return
-        secs = _time_graph(torch, launch, K, W)
+        times = _time_graph(torch, launch, K, W)
+        secs = _median(times)
         n_params = 2 + (Kt is not None)  # temperature, top_p (+ top_k) per row
         alg = wlmod.algorithmic_bytes_sampling(B, V, x0.element_size(), n_params)
         rows_per_s = B * K / secs
         per_launch = secs / K
         cpu = None
         if not a.no_cpu_baseline:
-            rows = a.cpu_rows or B
-            v, cores = _cpu_baseline_sampling(wl, rows)
-            cpu = {"value": v, "unit": "rows/s", "cores": cores, "kind": "port",
-                   "sample": f"first {rows} rows of the same {B}x{V} workload, float64 C oracle, 1 thread"}
+            rows = a.cpu_rows or 128
+            r = _cpu_baseline_sampling(torch, wl, rows, seconds=5.0)
+            (na, va), (_, v1) = list(r.items())[0], list(r.items())[-1]
+            cpu = {"value": va, "unit": "rows/s", "cores": na, "kind": "port",
+                   "value_1_core": v1, "cores_1_core": 1,
+                   "sample": f"first {rows} rows of the same {B}x{V} workload, repeated for 5 s per thread "
+                             "count: torch on the CPU (softmax, descending sort, cumsum top-k/top-p, "
+                             "inverse CDF by searchsorted)"}
         result = {
             "metric": METRIC,
             "value": rows_per_s,
@@ -241,6 +350,7 @@ def main():
             "data": "synthetic",
             "config": {"workload": desc, "batch": B, "vocab": V, "logits_dtype": str(x0.dtype).split(".")[-1],
                        "rotated_buffers": nbuf, "rotated_bytes": nbuf * buf_bytes},
+            "timing": _timing(times, K),
             "roofline": {
                 "bound": "hbm",
                 "achieved": alg / per_launch / 1e9,
@@ -255,7 +365,7 @@ def main():
         wl = wlmod.gate_cdb(dev)
         gate = pkg.OuroExitGate(wl["weight"], wl["bias"], exit_threshold=wl["tau"], loop_steps=4)
         B, H = wl["hidden"][0].shape
-        nset = 64  # 64 x 4 steps x 2 MiB hidden states rotate through > 512 MB
+        nset = 320  # 320 hidden-state sets of 2 MiB: 640 MiB rotate, beyond the 256 MB Infinity Cache
         hs = [torch.randn(B, H, device=dev).to(torch.bfloat16) for _ in range(nset)]
         F = torch.zeros(B, device=dev)
 
@@ -265,18 +375,29 @@ def main():
         if a.traffic_probe:
             _probe(torch, launch, dev)
             return
-        secs = _time_graph(torch, launch, K, W)
+        times = _time_graph(torch, launch, K, W)
+        secs = _median(times)
         per = secs / K
         alg = wlmod.algorithmic_bytes_gate(B, H)
+        cpu = None
+        if not a.no_cpu_baseline:
+            r = _cpu_baseline_gate(torch, wl, seconds=3.0)
+            (na, va), (_, v1) = list(r.items())[0], list(r.items())[-1]
+            cpu = {"value": va, "unit": "steps/s", "cores": na, "kind": "port", "value_1_core": v1,
+                   "cores_1_core": 1,
+                   "sample": "the same 4 gate steps (B=512, H=2048 bf16), repeated for 3 s per thread count: "
+                             "torch on the CPU (F.linear, sigmoid update, threshold, nonzero compaction)"}
         result = {
             "metric": "exit-gate steps/sec (B=512, H=2048 bf16, with compaction)",
             "value": K / secs, "unit": "steps/s", "n_gpus": 1, "steps": K, "warmup": W,
             "ms_per_step": per * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "gate_cdb: B=512 H=2048 bf16, tau=0.2, 4 loop steps", "batch": B, "hidden": H},
+            "config": {"workload": "gate_cdb: B=512 H=2048 bf16, tau=0.2, 4 loop steps", "batch": B, "hidden": H,
+                       "rotated_sets": nset},
+            "timing": _timing(times, K),
             "roofline": {"bound": "hbm", "achieved": alg / per / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": alg / per / 1e9 / HBM_PEAK_GBS, "traffic": _traffic_from_profiles(a.workload)},
-            "cpu_baseline": None,
+            "cpu_baseline": cpu,
         }
     print(json.dumps(result))
 

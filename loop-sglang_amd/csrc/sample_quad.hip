@@ -46,8 +46,10 @@ constexpr int kNT = 256;          // threads per row
 constexpr int kNW = kNT / kWave;  // waves per row
 constexpr int kHB = 128;          // coarse histogram: bins of 1/4 binary order over y in [-32, 0]
 constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order over y in [-32, 0]
-constexpr int kSeg = 128;         // window entries staged per wave
-constexpr int kWin = 256;         // window finished by one wave (4 entries per lane)
+constexpr int kSeg = 256;         // window entries staged per wave
+constexpr int kWin = 512;         // window finished by one wave
+constexpr int kHPL = kWin / kWave;  // window entries per lane in the finish
+constexpr int kStg = 128;         // candidate chunks staged per wave
 constexpr int kRB = 256;          // refinement bins per level
 constexpr int kVB = 512;          // value bins bracketing an exact top-p threshold
 constexpr int kCW = 384;          // bracket candidates per wave
@@ -140,8 +142,8 @@ struct Smem {
       uint64_t seg[kNW][kSeg];                    // window entries per wave, index order
       unsigned long long fmass[kFB];              // fine histogram: masses (2^-40 fixed point)
       uint32_t fcnt[kFB];                         // fine histogram: counts
-      v4u stg[kNW][kWave];                        // staged candidate chunks per wave, (column, lane) order
-      uint32_t smeta[kNW][kWave];                 // their column * 64 + lane
+      v4u stg[kNW][kStg];                         // staged candidate chunks per wave, (column, lane) order
+      uint32_t smeta[kNW][kStg];                  // their column * 64 + lane
     };
     struct {                                      // exact refinement and its inverse CDF
       unsigned long long rb[4][kRB + 1];          // refinement bins, four copies by lane
@@ -824,11 +826,11 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
 
 // Entry ranked r-th largest (1-based) among the window entries of one fine bin
 // (flag `inb` per slot); keys are unique.  Wave 0 only.
-__device__ __forceinline__ uint64_t bin_rank(const uint64_t (&key)[4], const bool (&inb)[4], int r) {
+__device__ __forceinline__ uint64_t bin_rank(const uint64_t (&key)[kHPL], const bool (&inb)[kHPL], int r) {
   uint64_t best = 0ull;
   bool done = false;
 #pragma unroll 1
-  for (int h = 0; h < 4 && !done; ++h) {
+  for (int h = 0; h < kHPL && !done; ++h) {
     uint64_t b = __ballot(inb[h]);
     while (b && !done) {
       const int l = __ffsll((unsigned long long)b) - 1;
@@ -837,7 +839,7 @@ __device__ __forceinline__ uint64_t bin_rank(const uint64_t (&key)[4], const boo
                           (uint32_t)__builtin_amdgcn_readlane((int)(key[h] & 0xffffffffu), l);
       int gt = 0;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) gt += (inb[g] && key[g] > kq) ? 1 : 0;
+      for (int g = 0; g < kHPL; ++g) gt += (inb[g] && key[g] > kq) ? 1 : 0;
       if (wave_sum_i(gt) == r - 1) {
         best = kq;
         done = true;
@@ -847,8 +849,8 @@ __device__ __forceinline__ uint64_t bin_rank(const uint64_t (&key)[4], const boo
   return best;
 }
 
-// Window finish by wave 0: entries q = h*64 + lane (h = 0..3) of the window
-// (nw <= 256, index order).  Threshold from the fine histograms, exact inside
+// Window finish by wave 0: lane l holds window positions kHPL*l .. kHPL*l + kHPL-1
+// (nw <= kWin, index order).  Threshold from the fine histograms, exact inside
 // the crossing bin; then the inverse CDF over the kept entries.
 template <int CAP>
 __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&cq)[kNW], float m, float c, double Z, bool kon,
@@ -858,14 +860,14 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
   base[0] = 0;
 #pragma unroll
   for (int q = 1; q < kNW; ++q) base[q] = base[q - 1] + cq[q - 1];
-  bool in[4];
-  uint64_t key[4];
-  uint32_t kx[4];
-  float e[4];
-  int fb[4];
+  bool in[kHPL];
+  uint64_t key[kHPL];
+  uint32_t kx[kHPL];
+  float e[kHPL];
+  int fb[kHPL];
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    const int q = 4 * lane + h;  // lane-major: lane l holds window positions 4l .. 4l+3
+  for (int h = 0; h < kHPL; ++h) {
+    const int q = kHPL * lane + h;  // lane-major
     in[h] = q < nw;
     int w = 0;
 #pragma unroll
@@ -901,13 +903,15 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
     *above = a;
     return true;
   };
-  bool inK[4] = {in[0], in[1], in[2], in[3]};
+  bool inK[kHPL];
+#pragma unroll
+  for (int h = 0; h < kHPL; ++h) inK[h] = in[h];
   if (kon) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) S.fcnt[4 * lane + q] = 0u;
     __builtin_amdgcn_s_waitcnt(0xc07f);
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
+    for (int h = 0; h < kHPL; ++h)
       if (in[h]) atomicAdd(&S.fcnt[fb[h]], 1u);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     double bv[4];
@@ -917,15 +921,15 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
     double above;
     const int kk = k < nw ? k : nw;
     if (crossing(bv, (double)kk, &bk, &above)) {
-      bool inb[4];
+      bool inb[kHPL];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) inb[h] = in[h] && fb[h] == bk;
+      for (int h = 0; h < kHPL; ++h) inb[h] = in[h] && fb[h] == bk;
       const uint64_t kth = bin_rank(key, inb, kk - (int)above);
       thr = (uint32_t)(kth >> 32);
     }
     double zk = 0.0;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
+    for (int h = 0; h < kHPL; ++h) {
       inK[h] = in[h] && kx[h] >= thr;
       zk += inK[h] ? (double)e[h] : 0.0;
     }
@@ -937,7 +941,7 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
     for (int q = 0; q < 4; ++q) S.fmass[4 * lane + q] = 0ull;
     __builtin_amdgcn_s_waitcnt(0xc07f);
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
+    for (int h = 0; h < kHPL; ++h)
       if (inK[h]) atomicAdd(&S.fmass[fb[h]], fix40(e[h]));
     __builtin_amdgcn_s_waitcnt(0xc07f);
     double bv[4];
@@ -947,21 +951,21 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
     double above;
     if (crossing(bv, target, &bp, &above)) {
       // distinct value keys of the crossing bin, from the top, until the target is met
-      bool rem[4];
+      bool rem[kHPL];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) rem[h] = inK[h] && fb[h] == bp;
+      for (int h = 0; h < kHPL; ++h) rem[h] = inK[h] && fb[h] == bp;
       double a = above;
       uint32_t t2 = thr;
 #pragma unroll 1
       for (int it = 0; it < kWin; ++it) {
         uint32_t mk = 0u;
 #pragma unroll
-        for (int h = 0; h < 4; ++h) mk = max(mk, rem[h] ? kx[h] : 0u);
+        for (int h = 0; h < kHPL; ++h) mk = max(mk, rem[h] ? kx[h] : 0u);
         const uint32_t vmax = (uint32_t)wave_max_i((int)(mk ^ 0x80000000u)) ^ 0x80000000u;
         if (vmax == 0u) break;
         double s = 0.0;
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int h = 0; h < kHPL; ++h) {
           const bool eq = rem[h] && kx[h] == vmax;
           s += eq ? (double)fix40(e[h]) : 0.0;
           rem[h] = rem[h] && !eq;
@@ -973,15 +977,17 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
       thr = max(thr, t2);
     }
   }
-  // inverse CDF over the kept entries in index order (positions 4l .. 4l+3 in lane l)
-  float ek[4];
-  bool kept[4];
+  // inverse CDF over the kept entries in index order (lane-major positions)
+  float ek[kHPL];
+  bool kept[kHPL];
+  bool anyk = false;
   double ls = 0.0;
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
+  for (int h = 0; h < kHPL; ++h) {
     kept[h] = inK[h] && kx[h] >= thr;
     ek[h] = kept[h] ? e[h] : 0.0f;
     ls += (double)ek[h];
+    anyk = anyk || kept[h];
   }
   const double inc = wave_incl_scan(ls, lane);
   const double U = (double)uni(u) * readlane_d(inc, 63);
@@ -989,7 +995,7 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
   {
     const uint64_t hit = __ballot(ls > 0.0 && inc > U);
     const uint64_t pos = __ballot(ls > 0.0);
-    const uint64_t any = __ballot(kept[0] || kept[1] || kept[2] || kept[3]);
+    const uint64_t any = __ballot(anyk);
     src = hit ? __ffsll((unsigned long long)hit) - 1
               : (pos ? 63 - __clzll((long long)pos) : (any ? 63 - __clzll((long long)any) : 0));
   }
@@ -997,7 +1003,7 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
     double a = inc - ls;
     int pick = -1, lastm = -1, lastk = 0;
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
+    for (int h = 0; h < kHPL; ++h) {
       if (kept[h]) lastk = h;
       if (ek[h] > 0.0f) {
         lastm = h;
@@ -1008,7 +1014,7 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
     if (pick < 0) pick = lastm >= 0 ? lastm : lastk;
     uint32_t lo = 0;
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
+    for (int h = 0; h < kHPL; ++h)
       if (h == pick) lo = (uint32_t)(key[h] & 0xffffffffu);
     *out = (int32_t)(0xffffffffu - lo);
   }
@@ -1212,7 +1218,7 @@ void quad_sample_kernel(SampleParams P) {
         const uint64_t bj = __ballot(hj);
         const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
-        if (hj && slot < kWave) {
+        if (hj && slot < kStg) {
           stg[slot] = R.d[j];
           meta[slot] = (uint32_t)(j * kWave + lane);
         }
@@ -1221,27 +1227,31 @@ void quad_sample_kernel(SampleParams P) {
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's staging writes are done
     __builtin_amdgcn_wave_barrier();
-    // B: lane i takes staged chunk i and writes its elements above the floor
-    if (ns <= kWave) {
-      const bool act = lane < ns;
-      const v4u v = stg[act ? lane : 0];
-      const uint32_t mt = meta[act ? lane : 0];
-      const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);  // chunk index in the row
-      float x[EPV];
-      QE<T>::unpack(v, x);
-      int cnt = 0;
+    // B: lane i takes staged chunks i and i + 64 and writes their elements
+    // above the floor (slot order is index order)
+    if (ns <= kStg) {
+#pragma unroll 1
+      for (int r0 = 0; r0 < ns; r0 += kWave) {
+        const bool act = r0 + lane < ns;
+        const v4u v = stg[act ? r0 + lane : 0];
+        const uint32_t mt = meta[act ? r0 + lane : 0];
+        const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);  // chunk index in the row
+        float x[EPV];
+        QE<T>::unpack(v, x);
+        int cnt = 0;
 #pragma unroll
-      for (int i = 0; i < EPV; ++i) cnt += (act && (x[i] - m) * c >= Lm) ? 1 : 0;
-      const int incl = wave_incl_scan_i(cnt, lane);
-      int pos = incl - cnt;
+        for (int i = 0; i < EPV; ++i) cnt += (act && (x[i] - m) * c >= Lm) ? 1 : 0;
+        const int incl = wave_incl_scan_i(cnt, lane);
+        int pos = run + incl - cnt;
 #pragma unroll
-      for (int i = 0; i < EPV; ++i) {
-        if (act && (x[i] - m) * c >= Lm) {
-          if (pos < kSeg) seg[pos] = ((uint64_t)okey(x[i]) << 32) | (uint64_t)(0xffffffffu - (ci * EPV + i));
-          ++pos;
+        for (int i = 0; i < EPV; ++i) {
+          if (act && (x[i] - m) * c >= Lm) {
+            if (pos < kSeg) seg[pos] = ((uint64_t)okey(x[i]) << 32) | (uint64_t)(0xffffffffu - (ci * EPV + i));
+            ++pos;
+          }
         }
+        run += __builtin_amdgcn_readlane(incl, 63);
       }
-      run = __builtin_amdgcn_readlane(incl, 63);
     } else {
       run = kSeg + 1;  // too many candidate chunks: the exact path decides
     }
