@@ -33,6 +33,8 @@
 //     exact radix refinement over the row.
 // Sums above the chunk level are float64; window masses are 2^-40 fixed point,
 // so the threshold sums are exact and independent of atomic order.
+#include <type_traits>
+
 #include "lsg_capi_internal.h"
 #include "lsg_common.h"
 #include "lsg_sample.h"
@@ -42,17 +44,22 @@
 namespace lsg {
 namespace quad {
 
-constexpr int kNT = 256;          // threads per row
-constexpr int kNW = kNT / kWave;  // waves per row
+// A row is held by NW waves (NW * 64 threads, CAP 16-byte chunks per lane);
+// the per-wave capacities of the window and of the exact top-p candidates
+// shrink as NW grows, so their row totals stay fixed.
+constexpr int seg_cap(int nw) { return 1024 / nw; }   // window entries staged per wave
+constexpr int stg_cap(int nw) { return 512 / nw; }    // candidate chunks staged per wave
+constexpr int cand_cap(int nw) { return 1536 / nw; }  // exact top-p candidates per wave
+// Waves per SIMD the kernels are compiled for: three four-wave or one
+// twelve-wave row (168 registers), one eight-wave row (256), or one
+// sixteen-wave row (128).
+constexpr int waves_per_eu(int nw) { return nw == 16 ? 4 : nw == 8 ? 2 : 3; }
 constexpr int kHB = 128;          // coarse histogram: bins of 1/4 binary order over y in [-32, 0]
 constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order over y in [-32, 0]
-constexpr int kSeg = 256;         // window entries staged per wave
 constexpr int kWin = 512;         // window finished by one wave
 constexpr int kHPL = kWin / kWave;  // window entries per lane in the finish
-constexpr int kStg = 128;         // candidate chunks staged per wave
 constexpr int kRB = 256;          // refinement bins per level
 constexpr int kVB = 512;          // value bins bracketing an exact top-p threshold
-constexpr int kCW = 384;          // bracket candidates per wave
 constexpr double kFix = 1099511627776.0;  // 2^40
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kNonTemporal = 2;   // buffer-load cache policy: stream through the caches
@@ -133,39 +140,39 @@ __device__ __forceinline__ float tree_sum(float (&e)[N]) {
   return e[0];
 }
 
-template <int CAP>
+template <int CAP, int NW>
 struct Smem {
-  uint32_t cm[kNT][CAP / 2 + 1];  // chunk-maximum upper bounds, two 16-bit patterns per word (odd stride: no bank conflicts)
-  uint32_t wh[kNW][kHB];      // per-wave coarse histograms (count, or mass as float bits)
+  uint32_t cm[(NW * kWave)][CAP / 2 + 1];  // chunk-maximum upper bounds, two 16-bit patterns per word (odd stride: no bank conflicts)
+  uint32_t wh[NW][kHB];      // per-wave coarse histograms (count, or mass as float bits)
   union {
     struct {                                      // top-k / top-p window
-      uint64_t seg[kNW][kSeg];                    // window entries per wave, index order
+      uint64_t seg[NW][seg_cap(NW)];                    // window entries per wave, index order
       unsigned long long fmass[kFB];              // fine histogram: masses (2^-40 fixed point)
       uint32_t fcnt[kFB];                         // fine histogram: counts
-      v4u stg[kNW][kStg];                         // staged candidate chunks per wave, (column, lane) order
-      uint32_t smeta[kNW][kStg];                  // their column * 64 + lane
+      v4u stg[NW][stg_cap(NW)];                         // staged candidate chunks per wave, (column, lane) order
+      uint32_t smeta[NW][stg_cap(NW)];                  // their column * 64 + lane
     };
     struct {                                      // exact refinement and its inverse CDF
       unsigned long long rb[4][kRB + 1];          // refinement bins, four copies by lane
-      double colsum[kNW][CAP];                    // kept mass per wave and chunk column
+      double colsum[NW][CAP];                    // kept mass per wave and chunk column
     };
     struct {                                      // exact top-p, pass 1
-      uint32_t vh[kNW][kVB + 1];                  // value histograms per wave (bin kVB: sink), 2^-16 of the bin top
+      uint32_t vh[NW][kVB + 1];                  // value histograms per wave (bin kVB: sink), 2^-16 of the bin top
     };
     struct {                                      // exact top-p, pass 2 and the threshold
-      uint32_t ckey[kNW][kCW];                    // bracket candidates per wave: order key >> SH,
-      float cmass[kNW][kCW];                      //   mass,
-      uint32_t cpos[kNW][kCW];                    //   (column * 64 + lane) * 8 + element
+      uint32_t ckey[NW][cand_cap(NW)];                    // bracket candidates per wave: order key >> SH,
+      float cmass[NW][cand_cap(NW)];                      //   mass,
+      uint32_t cpos[NW][cand_cap(NW)];                    //   (column * 64 + lane) * 8 + element
       double kbin[kRB];                           // key bins (masses)
-      double ksum[kNW][CAP];                      // kept mass per wave and chunk column
+      double ksum[NW][CAP];                      // kept mass per wave and chunk column
     };
   };
-  float wmax[kNW];
-  double wz[kNW];
-  double red[kNW];
+  float wmax[NW];
+  double wz[NW];
+  double red[NW];
   double rz;
-  v4u lt[kNT];  // per lane: largest, second-largest chunk maximum, chunk of the largest
-  int cnt[kNW];
+  v4u lt[(NW * kWave)];  // per lane: largest, second-largest chunk maximum, chunk of the largest
+  int cnt[NW];
   int imin;
 };
 
@@ -204,18 +211,32 @@ struct Row {
 };
 
 // Chunk-maximum upper bound j of this thread, from LDS.
-template <int CAP>
-__device__ __forceinline__ float cm_at(const Smem<CAP>& S, int j) {
+template <int CAP, int NW>
+__device__ __forceinline__ float cm_at(const Smem<CAP, NW>& S, int j) {
   const uint32_t w = S.cm[threadIdx.x][j >> 1];
   return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
 }
 
 // f(j, chunk, keep) over this lane's chunks re-read from memory, eight loads
-// in flight at a time; chunks whose maximum bound fails keep() in every lane of
-// the wave are skipped (and not loaded by the lanes that fail it).
-template <typename T, int CAP, class K, class F>
-__device__ __forceinline__ void each_chunk_mem(const Row<T, CAP>& R, const Smem<CAP>& S, K&& keep, F&& f) {
+// in flight at a time (rows of at most eight chunks per lane are read from
+// their register copy); chunks whose maximum bound fails keep() in every lane
+// of the wave are skipped (and not loaded by the lanes that fail it).
+template <typename T, int CAP, class K, class F, int NW>
+__device__ __forceinline__ void each_chunk_mem(const Row<T, CAP>& R, const Smem<CAP, NW>& S, K&& keep, F&& f) {
   static_assert(CAP % 8 == 0, "chunks are re-read in groups of eight");
+  if constexpr (CAP <= 8 && (NW <= 12 || std::is_same<T, bf16_t>::value)) {
+    // a short row stays in registers: no re-read (values unpacked by an
+    // earlier pass are recomputed, not kept live); sixteen-wave rows other
+    // than bf16 keep re-reading (their 128-register budget)
+    R.launder();
+#pragma unroll
+    for (int j = 0; j < CAP; ++j) {
+      const bool kp = keep(cm_at(S, j));
+      if (__ballot(kp)) f(j, R.d[j], kp);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
 #pragma unroll 1
   for (int jb = 0; jb < CAP; jb += 8) {
     v4u v[8];
@@ -241,8 +262,8 @@ struct LaneStats {
 // masses rescaled to it, two largest chunk maxima, chunk-maximum bounds to LDS.
 // NANIGN: NaN elements are ignored (a second pass for rows holding NaN);
 // otherwise NaN propagates into the maximum and marks the row for that pass.
-template <bool NANIGN, typename T, int CAP>
-__device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP>& S) {
+template <bool NANIGN, typename T, int CAP, int NW>
+__device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP, NW>& S) {
   constexpr int EPV = QE<T>::EPV;
   LaneStats s{-INFINITY, -INFINITY, -INFINITY, 0, 0.0};
   uint32_t pk = 0;
@@ -307,19 +328,21 @@ __device__ __forceinline__ float lane_max(const Row<T, CAP>& R, int* fj) {
 }
 
 // Sum of one double per wave over the workgroup, in wave order (all waves call).
-template <int CAP>
-__device__ __forceinline__ double wg_sum(Smem<CAP>& S, double wv) {
+template <int CAP, int NW>
+__device__ __forceinline__ double wg_sum(Smem<CAP, NW>& S, double wv) {
   if ((threadIdx.x & 63) == 0) S.red[threadIdx.x >> 6] = wv;
   __syncthreads();
-  const double r = ((S.red[0] + S.red[1]) + S.red[2]) + S.red[3];
+  double r = S.red[0];
+#pragma unroll
+  for (int q = 1; q < NW; ++q) r += S.red[q];
   __syncthreads();
   return r;
 }
 
 // torch.argmax over the row (first maximum; the first NaN if any): every wave calls.
 // MEM: the chunks are re-read from memory (a rare path of the sampling kernel).
-template <bool MEM, typename T, int CAP>
-__device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP>& S, int32_t* out) {
+template <bool MEM, typename T, int CAP, int NW>
+__device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP, NW>& S, int32_t* out) {
   constexpr int EPV = QE<T>::EPV;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int fj;
@@ -329,7 +352,10 @@ __device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP>& S, i
   if (threadIdx.x == 0) S.imin = 0x7fffffff;
   if (lane == 0) S.wmax[wid] = wm;
   __syncthreads();
-  const float m = uni(fmx(fmx(S.wmax[0], S.wmax[1]), fmx(S.wmax[2], S.wmax[3])));
+  float mw = S.wmax[0];
+#pragma unroll
+  for (int q = 1; q < NW; ++q) mw = fmx(mw, S.wmax[q]);
+  const float m = uni(mw);
   const bool isn = m != m;
   const bool cand = isn ? (ml != ml) : (ml == m);
   // the chunk where this lane first reached the maximum (from registers:
@@ -362,26 +388,45 @@ __device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP>& S, i
   if (threadIdx.x == 0) *out = S.imin;
 }
 
+// Wave q's mass in the row frame (maximum m), recomputed from the published
+// wave summaries wherever needed (identical in every wave; keeping the waves'
+// masses live across the tail would cost registers the row needs).
+template <int CAP, int NW>
+__device__ __forceinline__ double wave_mass(const Smem<CAP, NW>& S, int q, float m, float c) {
+  return S.wz[q] * (double)ex2c((S.wmax[q] - m) * c);
+}
+
 // Inverse CDF in index order (wave, chunk column j, lane, element) over
 // kept masses.  The crossing wave of U = u * Z comes from the waves' masses Zq
 // (identical in every wave); the others return.  Sets *Uw (mass to go from
 // the start of the crossing wave).
-__device__ __forceinline__ int cross_wave(const double (&Zq)[kNW], float u, double* Uw) {
-  const double Z = ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3];
+// Sum over the waves, in wave order, of zq(q) (a wave's mass read from LDS).
+template <int NW, class ZQ>
+__device__ __forceinline__ double wave_total(ZQ&& zq) {
+  double z = zq(0);
+#pragma unroll
+  for (int q = 1; q < NW; ++q) z += zq(q);
+  return z;
+}
+
+template <int NW, class ZQ>
+__device__ __forceinline__ int cross_wave(ZQ&& zq, float u, double* Uw) {
+  const double Z = wave_total<NW>(zq);
   const double U = (double)uni(u) * Z;
   int ws = -1, wl = 0;
   double acc = 0.0, bw = 0.0, bl = 0.0;
 #pragma unroll
-  for (int q = 0; q < kNW; ++q) {
-    if (Zq[q] > 0.0) {
+  for (int q = 0; q < NW; ++q) {
+    const double z = zq(q);
+    if (z > 0.0) {
       wl = q;
       bl = acc;
     }
-    if (ws < 0 && acc + Zq[q] > U) {
+    if (ws < 0 && acc + z > U) {
       ws = q;
       bw = acc;
     }
-    acc += Zq[q];
+    acc += z;
   }
   if (ws < 0) {  // u >= 1 or rounding: the last wave with mass
     ws = wl;
@@ -435,13 +480,13 @@ __device__ __forceinline__ void finish_column(const v4u& v, int ws, int js, doub
 // columns in flight at a time, sums the columns in order until U is crossed,
 // then finishes that column.  (The register copy of the row is left to the
 // top-k / top-p path, which needs it on every row.)
-template <typename T, int CAP, class EM>
-__device__ __forceinline__ void walk_cols(const Row<T, CAP>& R, const double (&Zq)[kNW], float u, EM&& emass,
-                                          int32_t* out) {
+template <typename T, int CAP, class EM, int NW>
+__device__ __forceinline__ void walk_cols(const Row<T, CAP>& R, const Smem<CAP, NW>& S, float m, float c, float u,
+                                          EM&& emass, int32_t* out) {
   constexpr int EPV = QE<T>::EPV;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   double Uw;
-  const int ws = cross_wave(Zq, u, &Uw);
+  const int ws = cross_wave<NW>([&](int q) { return wave_mass(S, q, m, c); }, u, &Uw);
   if (wid != ws) return;
   double acc = 0.0, accl = 0.0;
   int js = -1, jl = 0;
@@ -495,8 +540,8 @@ __device__ __forceinline__ float key_value(uint32_t kk) {
 // [lo, hi) holding the boundary into 256 bins (one LDS atomic per member, four
 // bin copies picked by lane); the scan from the top with the totals above the
 // bracket picks the bin; down to one key (ties kept).  Every wave calls.
-template <typename T, int CAP>
-__device__ __forceinline__ bool refine(const Row<T, CAP>& R, Smem<CAP>& S, float m, float c, float Lm, float xmin, bool kon,
+template <typename T, int CAP, int NW>
+__device__ __forceinline__ bool refine(const Row<T, CAP>& R, Smem<CAP, NW>& S, float m, float c, float Lm, float xmin, bool kon,
                        double target, uint32_t* thr_key) {
   constexpr int EPV = QE<T>::EPV, SH = QE<T>::SH;
   const int t = threadIdx.x, lane = t & 63;
@@ -506,7 +551,7 @@ __device__ __forceinline__ bool refine(const Row<T, CAP>& R, Smem<CAP>& S, float
     if (hi <= lo) return false;
     int sh = 0;
     while (((hi - lo - 1u) >> sh) >= (uint32_t)kRB) ++sh;
-    for (int i = t; i < 4 * (kRB + 1); i += kNT) (&S.rb[0][0])[i] = 0ull;
+    for (int i = t; i < 4 * (kRB + 1); i += (NW * kWave)) (&S.rb[0][0])[i] = 0ull;
     __syncthreads();
     const uint32_t lo_ = lo, hi_ = hi;
     const float xlo = key_value(lo << SH);
@@ -560,14 +605,14 @@ __device__ __forceinline__ bool refine(const Row<T, CAP>& R, Smem<CAP>& S, float
   return false;
 }
 
-template <typename T, int CAP>
-__device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP>& S, const double (*colsum)[CAP], float m,
+template <typename T, int CAP, int NW>
+__device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP, NW>& S, const double (*colsum)[CAP], float m,
                                           float c, float thr, float u, int32_t* out);
 
 // Fallback for top-k / top-p rows without a usable window: exact refinement,
 // then the inverse CDF over {x >= thr} with fresh masses.  Every wave calls.
-template <typename T, int CAP>
-__device__ __forceinline__ void row_exact(const Row<T, CAP>& R, Smem<CAP>& S, float m, float c, double Z, bool kon, int32_t k,
+template <typename T, int CAP, int NW>
+__device__ __forceinline__ void row_exact(const Row<T, CAP>& R, Smem<CAP, NW>& S, float m, float c, double Z, bool kon, int32_t k,
                           bool pon, float p, float Lm, float u, int32_t* out) {
   constexpr int EPV = QE<T>::EPV;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -611,8 +656,8 @@ __device__ __forceinline__ void row_exact(const Row<T, CAP>& R, Smem<CAP>& S, fl
 
 // Inverse CDF over the kept elements {x >= thr} given their mass per wave and
 // chunk column (this wave's row of colsum complete and visible to it).
-template <typename T, int CAP>
-__device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP>& S, const double (*colsum)[CAP], float m,
+template <typename T, int CAP, int NW>
+__device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP, NW>& S, const double (*colsum)[CAP], float m,
                                           float c, float thr, float u, int32_t* out) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   auto emass = [&](float x) { return x >= thr ? ex2c((x - m) * c) : 0.0f; };
@@ -620,9 +665,8 @@ __device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP>& S, co
   const double cinc = wave_incl_scan(cs, lane);
   if (lane == 63) S.wz[wid] = cinc;
   __syncthreads();
-  const double Zq[kNW] = {S.wz[0], S.wz[1], S.wz[2], S.wz[3]};
   double Uw;
-  const int ws = cross_wave(Zq, u, &Uw);
+  const int ws = cross_wave<NW>([&](int q) { return S.wz[q]; }, u, &Uw);
   if (wid != ws) return;
   int js;
   {
@@ -647,9 +691,9 @@ __device__ __forceinline__ void kept_draw(const Row<T, CAP>& R, Smem<CAP>& S, co
 // where key bins settle the exact threshold key; the kept candidates' masses
 // then join their columns and the inverse CDF runs as in row_exact.  Returns
 // false (uniformly, having written nothing) when the bracket cannot be formed
-// or its candidates overflow kCW per wave.  Every wave calls.
-template <typename T, int CAP>
-__device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S, float m, float c, double Z, float p,
+// or its candidates overflow cand_cap(NW) per wave.  Every wave calls.
+template <typename T, int CAP, int NW>
+__device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP, NW>& S, float m, float c, double Z, float p,
                                               float Lm, float u, int64_t V, int32_t* out) {
   constexpr int EPV = QE<T>::EPV, SH = QE<T>::SH;
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
@@ -660,7 +704,7 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
   const float s = (float)kVB / -ylo, w = -ylo / (float)kVB;
   auto vbin = [&](float y) { return min(kVB - 1, (int)(-y * s)); };
   // pass 1: value histograms
-  for (int i = t; i < kNW * (kVB + 1); i += kNT) (&S.vh[0][0])[i] = 0u;
+  for (int i = t; i < NW * (kVB + 1); i += (NW * kWave)) (&S.vh[0][0])[i] = 0u;
   __syncthreads();
   {
     uint32_t* vh = S.vh[wid];
@@ -685,7 +729,9 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int b = 8 * lane + q;
-      const uint64_t hsum = (uint64_t)S.vh[0][b] + S.vh[1][b] + S.vh[2][b] + S.vh[3][b];
+      uint64_t hsum = 0;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) hsum += S.vh[q][b];
       bm[q] = (double)hsum * (double)__builtin_amdgcn_exp2f(-((float)b * w)) * 0x1p-16;
       ls += bm[q];
     }
@@ -731,7 +777,7 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
       if (bal) {
         const int pos = nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        if (cd && pos < kCW) {
+        if (cd && pos < cand_cap(NW)) {
           S.ckey[wid][pos] = okey(x[i]) >> SH;
           S.cmass[wid][pos] = ei;
           S.cpos[wid][pos] = ((uint32_t)(j * kWave + lane) << 3) | (uint32_t)i;
@@ -744,18 +790,18 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
   });
   if (lane == 0) S.cnt[wid] = nc;
   __syncthreads();
-  int cq[kNW];
+  int cq[NW];
   bool ovf = false;
 #pragma unroll
-  for (int q = 0; q < kNW; ++q) {
+  for (int q = 0; q < NW; ++q) {
     cq[q] = uni(S.cnt[q]);
-    ovf = ovf || cq[q] > kCW;
+    ovf = ovf || cq[q] > cand_cap(NW);
   }
   if (ovf) return false;
   // mass above the bracket: every kept column sum so far
   double above = 0.0;
 #pragma unroll
-  for (int q = 0; q < kNW; ++q) {
+  for (int q = 0; q < NW; ++q) {
     const double cs = lane < CAP ? S.ksum[q][lane] : 0.0;
     above += wave_sum(cs);
   }
@@ -774,9 +820,9 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
     while (((hi - lo - 1u) >> sh) >= (uint32_t)kRB) ++sh;
     if (t < kRB) S.kbin[t] = 0.0;
     __syncthreads();
-    for (int q = t; q < kNW * kCW; q += kNT) {
-      const int cw = q / kCW, ci = q - cw * kCW;
-      if (ci < cq[cw]) {
+    for (int q = t; q < NW * cand_cap(NW); q += (NW * kWave)) {
+      const int cw = q / cand_cap(NW), ci = q - cw * cand_cap(NW);
+      if (ci < S.cnt[cw]) {
         const uint32_t key = S.ckey[cw][ci];
         if (key >= lo && key < hi) atomicAdd(&S.kbin[(hi - 1u - key) >> sh], (double)S.cmass[cw][ci]);
       }
@@ -814,9 +860,9 @@ __device__ __forceinline__ bool row_topp_fast(const Row<T, CAP>& R, Smem<CAP>& S
   }
   if (!found) return false;
   // the kept candidates join their columns
-  for (int q = t; q < kNW * kCW; q += kNT) {
-    const int cw = q / kCW, ci = q - cw * kCW;
-    if (ci < cq[cw] && S.ckey[cw][ci] >= thr_key)
+  for (int q = t; q < NW * cand_cap(NW); q += (NW * kWave)) {
+    const int cw = q / cand_cap(NW), ci = q - cw * cand_cap(NW);
+    if (ci < S.cnt[cw] && S.ckey[cw][ci] >= thr_key)
       atomicAdd(&S.ksum[cw][(S.cpos[cw][ci] >> 3) / kWave], (double)S.cmass[cw][ci]);
   }
   __syncthreads();
@@ -852,14 +898,14 @@ __device__ __forceinline__ uint64_t bin_rank(const uint64_t (&key)[kHPL], const 
 // Window finish by wave 0: lane l holds window positions kHPL*l .. kHPL*l + kHPL-1
 // (nw <= kWin, index order).  Threshold from the fine histograms, exact inside
 // the crossing bin; then the inverse CDF over the kept entries.
-template <int CAP>
-__device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&cq)[kNW], float m, float c, double Z, bool kon,
+template <int CAP, int NW>
+__device__ __forceinline__ void window_finish(Smem<CAP, NW>& S, int nw, const int (&cq)[NW], float m, float c, double Z, bool kon,
                               int32_t k, bool pon, float p, float u, int32_t* out) {
   const int lane = threadIdx.x & 63;
-  int base[kNW];
+  int base[NW];
   base[0] = 0;
 #pragma unroll
-  for (int q = 1; q < kNW; ++q) base[q] = base[q - 1] + cq[q - 1];
+  for (int q = 1; q < NW; ++q) base[q] = base[q - 1] + cq[q - 1];
   bool in[kHPL];
   uint64_t key[kHPL];
   uint32_t kx[kHPL];
@@ -869,10 +915,14 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
   for (int h = 0; h < kHPL; ++h) {
     const int q = kHPL * lane + h;  // lane-major
     in[h] = q < nw;
-    int w = 0;
+    int w = 0, off = q;
 #pragma unroll
-    for (int g = 1; g < kNW; ++g) w = q >= base[g] ? g : w;
-    key[h] = in[h] ? S.seg[w][q - base[w]] : 0ull;
+    for (int g = 1; g < NW; ++g) {
+      const bool ge = q >= base[g];
+      w = ge ? g : w;
+      off = ge ? q - base[g] : off;
+    }
+    key[h] = in[h] ? S.seg[w][off] : 0ull;
     kx[h] = (uint32_t)(key[h] >> 32);
     const float x = okey_inv(kx[h]);
     const float y = (x - m) * c;
@@ -1020,18 +1070,10 @@ __device__ __forceinline__ void window_finish(Smem<CAP>& S, int nw, const int (&
   }
 }
 
-// The waves' masses in the row frame (maximum m), recomputed from the published
-// wave summaries wherever needed (identical in every wave; keeping them live
-// across the tail would cost registers the row needs).
-template <int CAP>
-__device__ __forceinline__ void wave_masses(const Smem<CAP>& S, float m, float c, double (&Zq)[kNW]) {
-#pragma unroll
-  for (int q = 0; q < kNW; ++q) Zq[q] = S.wz[q] * (double)ex2c((S.wmax[q] - m) * c);
-}
 
 // Row statistics after the pass, published per wave before barrier 1.
-template <typename T, int CAP>
-__device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, bool pon, Smem<CAP>& S) {
+template <typename T, int CAP, int NW>
+__device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, bool pon, Smem<CAP, NW>& S) {
   constexpr int N = CAP * QE<T>::EPV;  // elements per lane
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const float wm = wave_maximum(s.ml);
@@ -1067,11 +1109,11 @@ __device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, b
   if (kon || pon) S.lt[threadIdx.x] = v4u{__float_as_uint(s.t1), __float_as_uint(s.t2), (uint32_t)s.j1, 0u};
 }
 
-template <typename T, int CAP>
-__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3)))
+template <typename T, int CAP, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(waves_per_eu(NW))))
 void quad_sample_kernel(SampleParams P) {
   constexpr int EPV = QE<T>::EPV;
-  __shared__ Smem<CAP> S;
+  __shared__ Smem<CAP, NW> S;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int64_t nrows = P.B_out;
   if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
@@ -1103,24 +1145,23 @@ void quad_sample_kernel(SampleParams P) {
   const bool tvalid = Tr > 0.0f && Tr < INFINITY;
   const float c = tvalid ? kLog2e / Tr : 1.0f;
   const bool kon = k >= 1 && (int64_t)k < P.V, pon = p < 1.0f;
-  float wq[kNW] = {0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY;
   if (tvalid) {
     if (kon || pon) S.wh[wid][lane] = S.wh[wid][lane + kWave] = 0u;  // this wave's histogram (a wave's LDS ops stay in order)
     publish<T, CAP>(lane_pass<false>(R, c, S), c, kon, pon, S);
     __syncthreads();
+    m = S.wmax[0];
 #pragma unroll
-    for (int q = 0; q < kNW; ++q) wq[q] = uni(S.wmax[q]);
-    m = fmx(fmx(wq[0], wq[1]), fmx(wq[2], wq[3]));
+    for (int q = 1; q < NW; ++q) m = fmx(m, S.wmax[q]);
     if (m != m) {
       // NaN present: NaN carries no mass; pass again ignoring it
       __syncthreads();
       if (kon || pon) S.wh[wid][lane] = S.wh[wid][lane + kWave] = 0u;
       publish<T, CAP>(lane_pass<true>(R, c, S), c, kon, pon, S);
       __syncthreads();
+      m = S.wmax[0];
 #pragma unroll
-      for (int q = 0; q < kNW; ++q) wq[q] = uni(S.wmax[q]);
-      m = fmaxf(fmaxf(wq[0], wq[1]), fmaxf(wq[2], wq[3]));
+      for (int q = 1; q < NW; ++q) m = fmaxf(m, S.wmax[q]);
     }
   }
   if (!tvalid || !(m > -INFINITY) || !(m < INFINITY)) {
@@ -1130,9 +1171,7 @@ void quad_sample_kernel(SampleParams P) {
   __builtin_amdgcn_s_setprio(2);
   m = uni(m);
   if (!kon && !pon) {
-    double Zq[kNW];
-    wave_masses(S, m, c, Zq);
-    walk_cols(R, Zq, u, [&](float x) { return ex2c((x - m) * c); }, out);
+    walk_cols(R, S, m, c, u, [&](float x) { return ex2c((x - m) * c); }, out);
     return;
   }
   // ---- top-k / top-p: floor from the merged histograms (row bin b gathers
@@ -1143,10 +1182,11 @@ void quad_sample_kernel(SampleParams P) {
     int pc[2] = {0, 0};
     float pmf[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (int q = 0; q < kNW; ++q) {
-      const float D = (m - wq[q]) * c;
+    for (int q = 0; q < NW; ++q) {
+      const float wmq = uni(S.wmax[q]);
+      const float D = (m - wmq) * c;
       const int sq = D < 32.0f ? (int)__builtin_ceilf(4.0f * D + 0x1p-8f) : kHB;
-      const float fq = ex2c((wq[q] - m) * c);
+      const float fq = ex2c((wmq - m) * c);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int idx = 2 * lane + h - sq;
@@ -1167,9 +1207,7 @@ void quad_sample_kernel(SampleParams P) {
         hb = before + __builtin_amdgcn_readlane(pc[0], lb) >= k ? 0 : 1;
       }
     } else {
-      double Zq[kNW];
-      wave_masses(S, m, c, Zq);
-      const double Zr = ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3];
+      const double Zr = wave_total<NW>([&](int q) { return wave_mass(S, q, m, c); });
       if (threadIdx.x == 0) S.rz = Zr;  // the row normaliser, for the window finish
       const double tgt = (double)p * Zr * kBinMargin;
       const double inc = wave_incl_scan((double)pmf[0] + (double)pmf[1], lane);
@@ -1218,7 +1256,7 @@ void quad_sample_kernel(SampleParams P) {
         const uint64_t bj = __ballot(hj);
         const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
-        if (hj && slot < kStg) {
+        if (hj && slot < stg_cap(NW)) {
           stg[slot] = R.d[j];
           meta[slot] = (uint32_t)(j * kWave + lane);
         }
@@ -1229,7 +1267,7 @@ void quad_sample_kernel(SampleParams P) {
     __builtin_amdgcn_wave_barrier();
     // B: lane i takes staged chunks i and i + 64 and writes their elements
     // above the floor (slot order is index order)
-    if (ns <= kStg) {
+    if (ns <= stg_cap(NW)) {
 #pragma unroll 1
       for (int r0 = 0; r0 < ns; r0 += kWave) {
         const bool act = r0 + lane < ns;
@@ -1246,44 +1284,42 @@ void quad_sample_kernel(SampleParams P) {
 #pragma unroll
         for (int i = 0; i < EPV; ++i) {
           if (act && (x[i] - m) * c >= Lm) {
-            if (pos < kSeg) seg[pos] = ((uint64_t)okey(x[i]) << 32) | (uint64_t)(0xffffffffu - (ci * EPV + i));
+            if (pos < seg_cap(NW)) seg[pos] = ((uint64_t)okey(x[i]) << 32) | (uint64_t)(0xffffffffu - (ci * EPV + i));
             ++pos;
           }
         }
         run += __builtin_amdgcn_readlane(incl, 63);
       }
     } else {
-      run = kSeg + 1;  // too many candidate chunks: the exact path decides
+      run = seg_cap(NW) + 1;  // too many candidate chunks: the exact path decides
     }
     if (lane == 0) S.cnt[wid] = run;
   }
   __syncthreads();
   if (bstar >= 0) {
-    int cq[kNW], nw = 0;
+    int cq[NW], nw = 0;
     bool ovf = false;
 #pragma unroll
-    for (int q = 0; q < kNW; ++q) {
+    for (int q = 0; q < NW; ++q) {
       cq[q] = uni(S.cnt[q]);
       nw += cq[q];
-      ovf = ovf || cq[q] > kSeg;
+      ovf = ovf || cq[q] > seg_cap(NW);
     }
     if (!ovf && nw <= kWin) {
       if (wid == 0) window_finish(S, nw, cq, m, c, (!kon && pon) ? S.rz : 0.0, kon, k, pon, p, u, out);
       return;
     }
   }
-  double Zq[kNW];
-  wave_masses(S, m, c, Zq);
-  const double Zr = ((Zq[0] + Zq[1]) + Zq[2]) + Zq[3];
+  const double Zr = wave_total<NW>([&](int q) { return wave_mass(S, q, m, c); });
   if (!kon && row_topp_fast(R, S, m, c, Zr, p, bstar >= 0 ? Lm : -INFINITY, u, P.V, out)) return;
   row_exact(R, S, m, c, Zr, kon, k, pon, p, bstar >= 0 ? Lm : -INFINITY, u, out);
 }
 
 // All-greedy batch: torch.argmax per row.
-template <typename T, int CAP>
-__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3)))
+template <typename T, int CAP, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(waves_per_eu(NW))))
 void quad_greedy_kernel(SampleParams P) {
-  __shared__ Smem<CAP> S;
+  __shared__ Smem<CAP, NW> S;
   int64_t nrows = P.B_out;
   if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
   const int64_t b = blockIdx.x;
@@ -1299,20 +1335,47 @@ void quad_greedy_kernel(SampleParams P) {
   row_argmax<false>(R, S, &P.out[b]);
 }
 
-template <typename T, int CAP>
+template <typename T, int CAP, int NW>
 static void launch(const SampleParams& P, bool greedy, hipStream_t st) {
-  if (greedy) hipLaunchKernelGGL((quad_greedy_kernel<T, CAP>), dim3((unsigned)P.B_out), dim3(kNT), 0, st, P);
-  else hipLaunchKernelGGL((quad_sample_kernel<T, CAP>), dim3((unsigned)P.B_out), dim3(kNT), 0, st, P);
+  if (greedy)
+    hipLaunchKernelGGL((quad_greedy_kernel<T, CAP, NW>), dim3((unsigned)P.B_out), dim3(NW * kWave), 0, st, P);
+  else
+    hipLaunchKernelGGL((quad_sample_kernel<T, CAP, NW>), dim3((unsigned)P.B_out), dim3(NW * kWave), 0, st, P);
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Row shapes held in registers: 4 waves x 32 or 24 chunks per lane (three rows
+// per compute unit); when the batch has no more rows than compute units, 16
+// or 12 waves x 8 chunks (one row per compute unit, all of its SIMDs busy);
+// fp32 rows of 65536 as 8 waves x 32 chunks (one row per compute unit).
 template <typename T>
 static bool launch_dtype(const SampleParams& P, bool greedy, hipStream_t st) {
   constexpr int EPV = QE<T>::EPV;
   if (P.V % EPV != 0) return false;
   const int64_t NV = P.V / EPV;
-  if (NV == (int64_t)kNT * 32) launch<T, 32>(P, greedy, st);
-  else if (NV == (int64_t)kNT * 24) launch<T, 24>(P, greedy, st);
-  else return false;
+  const bool small = P.B_out <= (int64_t)device_cus();
+  if (NV == 16 * kWave * 8 && small) launch<T, 8, 16>(P, greedy, st);
+  else if (NV == 12 * kWave * 8 && small) launch<T, 8, 12>(P, greedy, st);
+  else if (NV == 4 * kWave * 32) launch<T, 32, 4>(P, greedy, st);
+  else if (NV == 4 * kWave * 24) launch<T, 24, 4>(P, greedy, st);
+  else if constexpr (sizeof(T) == 4) {
+    if (NV == 8 * kWave * 32) launch<T, 32, 8>(P, greedy, st);
+    else return false;
+  } else {
+    return false;
+  }
   return true;
 }
 

@@ -123,7 +123,7 @@ def test_sample_mixed_depth_fp32(lsg, orc, dev):
 
 # --------------------------------------------------------------- edge cases --
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("V", [1, 3, 100, 1000, 8191, 40000, 65536, 150001])
+@pytest.mark.parametrize("V", [1, 3, 100, 1000, 8191, 24576, 32768, 40000, 49152, 65536, 150001])
 def test_modes_ragged(lsg, orc, dev, dtype, V):
     """Every filter combination on ragged V (partial tail chunks)."""
     g = torch.Generator(device=dev).manual_seed(1000 + V)
