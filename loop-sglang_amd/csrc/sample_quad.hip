@@ -49,11 +49,19 @@ namespace quad {
 // shrink as NW grows, so their row totals stay fixed.
 constexpr int seg_cap(int nw) { return 1024 / nw; }   // window entries staged per wave
 constexpr int stg_cap(int nw) { return 512 / nw; }    // candidate chunks staged per wave
-constexpr int cand_cap(int nw) { return 1536 / nw; }  // exact top-p candidates per wave
-// Waves per SIMD the kernels are compiled for: three four-wave or one
-// twelve-wave row (168 registers), one eight-wave row (256), or one
-// sixteen-wave row (128).
-constexpr int waves_per_eu(int nw) { return nw == 16 ? 4 : nw == 8 ? 2 : 3; }
+// exact top-p candidates per wave (four-wave rows: 1024, so that four rows fit
+// one compute unit's LDS)
+constexpr int cand_cap(int nw) { return nw == 4 ? 256 : 1536 / nw; }
+// Loads in flight per lane during the pass.  Rows of more than 16 chunks per
+// lane stream through a rolling window of 16 (the chunks are not kept: later
+// phases re-read the few they need), so that four four-wave rows, or two
+// eight-wave rows, are resident per compute unit; shorter rows are loaded whole
+// and stay in registers.
+constexpr int load_window(int cap) { return cap > 16 ? 16 : cap; }
+constexpr bool streams(int cap) { return load_window(cap) < cap; }
+// Waves per SIMD the kernels are compiled for (128 registers, or 168 for the
+// twelve-wave row of 8 chunks per lane, one row per compute unit).
+constexpr int waves_per_eu(int nw) { return nw == 12 ? 3 : 4; }
 constexpr int kHB = 128;          // coarse histogram: bins of 1/4 binary order over y in [-32, 0]
 constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order over y in [-32, 0]
 constexpr int kWin = 512;         // window finished by one wave
@@ -149,7 +157,8 @@ struct Smem {
       uint64_t seg[NW][seg_cap(NW)];                    // window entries per wave, index order
       unsigned long long fmass[kFB];              // fine histogram: masses (2^-40 fixed point)
       uint32_t fcnt[kFB];                         // fine histogram: counts
-      v4u stg[NW][stg_cap(NW)];                         // staged candidate chunks per wave, (column, lane) order
+      v4u stg[NW][streams(CAP) ? 1 : stg_cap(NW)];      // staged candidate chunks per wave, (column, lane) order
+                                                        //   (streamed rows re-read them instead)
       uint32_t smeta[NW][stg_cap(NW)];                  // their column * 64 + lane
     };
     struct {                                      // exact refinement and its inverse CDF
@@ -176,6 +185,13 @@ struct Smem {
   int imin;
 };
 
+// LDS of the all-greedy kernel.
+template <int NW>
+struct GSmem {
+  float wmax[NW];
+  int imin;
+};
+
 // A row in registers: CAP chunks per lane, wave-blocked.
 template <typename T, int CAP>
 struct Row {
@@ -189,10 +205,18 @@ struct Row {
                                            0x00020000);
     c0 = (uint32_t)(threadIdx.x >> 6) * (uint32_t)(CAP * kWave) + (threadIdx.x & 63);
   }
+  // Load j of this lane (streamed past the caches).
+  __device__ __forceinline__ void issue(int j) {
+    d[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(c0 * 16u), j * kWave * 16, kNonTemporal);
+  }
+  // The first load_window(CAP) loads; the pass issues the rest as it goes.
   __device__ __forceinline__ void fetch() {
 #pragma unroll
-    for (int j = 0; j < CAP; ++j)
-      d[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(c0 * 16u), j * kWave * 16, kNonTemporal);
+    for (int j = 0; j < load_window(CAP); ++j) issue(j);
+  }
+  // After chunk j is unpacked: the load that takes its place in the window.
+  __device__ __forceinline__ void roll(int j) {
+    if (j + load_window(CAP) < CAP) issue(j + load_window(CAP));
   }
   // Chunk `chunk` of the row re-read from memory (cold paths: the register
   // copy is then no longer needed, so those paths add no register pressure).
@@ -273,6 +297,7 @@ __device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP
     // NANIGN (rare rows holding NaN): chunks re-read from memory, so this pass
     // adds no register pressure to the register-resident row
     QE<T>::unpack(NANIGN ? R.load(j) : R.d[j], x);
+    if constexpr (!NANIGN) R.roll(j);
     float cm = x[0];
 #pragma unroll
     for (int i = 1; i < EPV; ++i) cm = NANIGN ? fmaxf(cm, x[i]) : fmx(cm, x[i]);
@@ -305,12 +330,15 @@ __device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP
 }
 
 // Maximum pass only (argmax): NaN-propagating lane maximum and the first chunk
-// at which it was reached (for NaN: the first chunk holding a NaN).
+// at which it was reached (for NaN: the first chunk holding a NaN).  A streamed
+// row keeps a copy of that chunk in *best as it goes.
 template <bool MEM, typename T, int CAP>
-__device__ __forceinline__ float lane_max(const Row<T, CAP>& R, int* fj) {
+__device__ __forceinline__ float lane_max(Row<T, CAP>& R, int* fj, v4u* best) {
   constexpr int EPV = QE<T>::EPV;
+  constexpr bool ST = !MEM && streams(CAP);
   float ml = -INFINITY;
   int f = 0;
+  v4u bv = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
     float x[EPV];
@@ -318,12 +346,23 @@ __device__ __forceinline__ float lane_max(const Row<T, CAP>& R, int* fj) {
     float cm = x[0];
 #pragma unroll
     for (int i = 1; i < EPV; ++i) cm = fmx(cm, x[i]);
-    f = (cm > ml || (cm != cm && ml == ml)) ? j : f;
+    // chunk 0 seeds the copy (a lane of -inf reaches its maximum there)
+    const bool hit = j == 0 || cm > ml || (cm != cm && ml == ml);
+    f = hit ? j : f;
+    if constexpr (ST) {
+      bv.x = hit ? R.d[j].x : bv.x;
+      bv.y = hit ? R.d[j].y : bv.y;
+      bv.z = hit ? R.d[j].z : bv.z;
+      bv.w = hit ? R.d[j].w : bv.w;
+      R.roll(j);
+    }
     ml = fmx(ml, cm);
-    asm volatile("" : "+v"(ml), "+v"(f));
+    if constexpr (ST) asm volatile("" : "+v"(ml), "+v"(f), "+v"(bv));
+    else asm volatile("" : "+v"(ml), "+v"(f));
     __builtin_amdgcn_sched_barrier(0);
   }
   *fj = f;
+  *best = bv;
   return ml;
 }
 
@@ -341,12 +380,13 @@ __device__ __forceinline__ double wg_sum(Smem<CAP, NW>& S, double wv) {
 
 // torch.argmax over the row (first maximum; the first NaN if any): every wave calls.
 // MEM: the chunks are re-read from memory (a rare path of the sampling kernel).
-template <bool MEM, typename T, int CAP, int NW>
-__device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP, NW>& S, int32_t* out) {
+template <bool MEM, int NW, typename T, int CAP, class SM>
+__device__ __forceinline__ void row_argmax(Row<T, CAP>& R, SM& S, int32_t* out) {
   constexpr int EPV = QE<T>::EPV;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int fj;
-  const float ml = lane_max<MEM>(R, &fj);
+  v4u best;
+  const float ml = lane_max<MEM>(R, &fj, &best);
   const float wm = wave_maximum(ml);
   __syncthreads();  // earlier readers of S are done
   if (threadIdx.x == 0) S.imin = 0x7fffffff;
@@ -363,6 +403,8 @@ __device__ __forceinline__ void row_argmax(const Row<T, CAP>& R, Smem<CAP, NW>& 
   v4u v = {0u, 0u, 0u, 0u};
   if constexpr (MEM) {
     v = R.load(fj);
+  } else if constexpr (streams(CAP)) {
+    v = best;
   } else {
 #pragma unroll
     for (int j = 0; j < CAP; ++j) {
@@ -1165,7 +1207,7 @@ void quad_sample_kernel(SampleParams P) {
     }
   }
   if (!tvalid || !(m > -INFINITY) || !(m < INFINITY)) {
-    row_argmax<true>(R, S, out);
+    row_argmax<true, NW>(R, S, out);
     return;
   }
   __builtin_amdgcn_s_setprio(2);
@@ -1244,8 +1286,9 @@ void quad_sample_kernel(SampleParams P) {
       }
     }
     const uint32_t cols = uni(wave_or(hm));
-    // A: the lanes holding a candidate chunk copy it to this wave's staging
-    // area, column by column (slots in (column, lane) = index order)
+    // A: the lanes holding a candidate chunk list it (and, for a row held in
+    // registers, copy it) in this wave's staging area, column by column (slots
+    // in (column, lane) = index order)
     v4u* stg = S.stg[wid];
     uint32_t* meta = S.smeta[wid];
     int ns = 0;
@@ -1257,7 +1300,7 @@ void quad_sample_kernel(SampleParams P) {
         const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
         if (hj && slot < stg_cap(NW)) {
-          stg[slot] = R.d[j];
+          if constexpr (!streams(CAP)) stg[slot] = R.d[j];
           meta[slot] = (uint32_t)(j * kWave + lane);
         }
         ns += (int)__popcll(bj);
@@ -1266,12 +1309,26 @@ void quad_sample_kernel(SampleParams P) {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's staging writes are done
     __builtin_amdgcn_wave_barrier();
     // B: lane i takes staged chunks i and i + 64 and writes their elements
-    // above the floor (slot order is index order)
+    // above the floor (slot order is index order); a streamed row gathers those
+    // chunks from memory, all rounds' loads at once
     if (ns <= stg_cap(NW)) {
-#pragma unroll 1
-      for (int r0 = 0; r0 < ns; r0 += kWave) {
+      constexpr int NR = (stg_cap(NW) + kWave - 1) / kWave;
+      v4u gv[NR];
+      if constexpr (streams(CAP)) {
+#pragma unroll
+        for (int rr = 0; rr < NR; ++rr) {
+          const int sl = rr * kWave + lane;
+          const uint32_t mt = meta[sl < ns ? sl : 0];
+          const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);
+          gv[rr] = sl < ns ? R.load_at(ci) : v4u{0u, 0u, 0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < NR; ++rr) {
+        const int r0 = rr * kWave;
+        if (r0 >= ns) break;
         const bool act = r0 + lane < ns;
-        const v4u v = stg[act ? r0 + lane : 0];
+        const v4u v = streams(CAP) ? gv[rr] : stg[act ? r0 + lane : 0];
         const uint32_t mt = meta[act ? r0 + lane : 0];
         const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);  // chunk index in the row
         float x[EPV];
@@ -1319,7 +1376,7 @@ void quad_sample_kernel(SampleParams P) {
 template <typename T, int CAP, int NW>
 __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(waves_per_eu(NW))))
 void quad_greedy_kernel(SampleParams P) {
-  __shared__ Smem<CAP, NW> S;
+  __shared__ GSmem<NW> S;
   int64_t nrows = P.B_out;
   if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
   const int64_t b = blockIdx.x;
@@ -1332,7 +1389,7 @@ void quad_greedy_kernel(SampleParams P) {
   Row<T, CAP> R;
   R.init(P.logits, r, P.ld, (uint32_t)P.V);
   R.fetch();
-  row_argmax<false>(R, S, &P.out[b]);
+  row_argmax<false, NW>(R, S, &P.out[b]);
 }
 
 template <typename T, int CAP, int NW>
