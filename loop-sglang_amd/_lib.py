@@ -42,6 +42,15 @@ _lib = None
 _lock = threading.Lock()
 
 
+def use_library(path: str) -> None:
+    """Load `path` (the phase-stamp profiling build) instead of the product
+    library; only before the first load()."""
+    global LIB_PATH
+    if _lib is not None:
+        raise RuntimeError(f"{LIB_NAME} is already loaded from {LIB_PATH}")
+    LIB_PATH = path
+
+
 def load() -> ctypes.CDLL:
     """Load the HIP library once; raise if it has not been built."""
     global _lib

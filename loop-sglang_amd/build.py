@@ -17,6 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB_NAME = "libloopsgl_tok.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+STAMPS_LIB_PATH = os.path.join(HERE, "libloopsgl_tok_stamps.so")
 ARCH = os.environ.get("LSG_OFFLOAD_ARCH", "gfx950")
 
 COMMON = [
@@ -44,16 +45,24 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libloopsgl_tok.so)")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link libloopsgl_tok.so; returns its path."""
-    os.makedirs(BUILD, exist_ok=True)
+def build(verbose: bool = False, stamps: bool = False) -> str:
+    """Compile every HIP source and link libloopsgl_tok.so; returns its path.
+
+    stamps=True builds the profiling variant instead, libloopsgl_tok_stamps.so:
+    the sampler records per-workgroup phase timestamps (-DLSG_PHASE_STAMPS),
+    read back by phase_stamps.py.  The product library is left untouched.
+    """
+    bdir = os.path.join(BUILD, "stamps") if stamps else BUILD
+    lib_path = STAMPS_LIB_PATH if stamps else LIB_PATH
+    os.makedirs(bdir, exist_ok=True)
     cc = hipcc()
     procs = []
     objs = []
     for src, extra in SOURCES.items():
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(bdir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmd = [cc, *COMMON, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+        flags = [*extra, "-DLSG_PHASE_STAMPS"] if stamps else extra
+        cmd = [cc, *COMMON, *flags, "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
@@ -70,14 +79,14 @@ def build(verbose: bool = False) -> str:
     if failed:
         msg = "\n".join(f"--- {s}\n{t}" for s, t in failed)
         raise RuntimeError(f"HIP build failed:\n{msg}")
-    tmp = LIB_PATH + ".tmp"
+    tmp = lib_path + ".tmp"
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, stamps="--stamps" in sys.argv))

@@ -39,8 +39,6 @@
 #include "lsg_common.h"
 #include "lsg_sample.h"
 
-#include <type_traits>
-
 namespace lsg {
 namespace quad {
 
@@ -75,6 +73,33 @@ constexpr int kNonTemporal = 2;   // buffer-load cache policy: stream through th
 // chunk maxima reach p*Z*(1 + 2^-10), so the window always reaches p*Z despite
 // the rounding of those sums.
 constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
+
+// Phase stamps, compiled in only by the profiling build (-DLSG_PHASE_STAMPS):
+// thread 0 of workgroup b writes the 100 MHz real-time counter at fixed points
+// of its row to g_phase_stamps[b * 8 + slot] (slots: 0 kernel entry, 1 wave 0's
+// pass done, 2 barrier 1 passed, 3 floor known, 4 candidates staged, 5 end,
+// 7 the row's first loads issued); slot 6 holds the hardware id (bits 0-31),
+// the XCC id (32-39) and the row's path (40-47: 1 window, 2 two-pass top-p,
+// 3 exact refinement, 4 unfiltered walk, 5 argmax, 6 small window).
+constexpr int kStampSlots = 8, kStampRows = 8192;
+enum StampPath { kPathWindow = 1, kPathTopp = 2, kPathExact = 3, kPathWalk = 4, kPathArgmax = 5, kPathSmall = 6 };
+#ifdef LSG_PHASE_STAMPS
+__device__ unsigned long long g_phase_stamps[kStampRows * kStampSlots];
+__device__ __forceinline__ void stamp_val(int slot, unsigned long long v) {
+  if (threadIdx.x == 0 && blockIdx.x < (unsigned)kStampRows) g_phase_stamps[blockIdx.x * kStampSlots + slot] = v;
+}
+__device__ __forceinline__ void stamp(int slot) { stamp_val(slot, __builtin_amdgcn_s_memrealtime()); }
+__device__ __forceinline__ void stamp_path(int path) {
+  // HW_ID (hwreg 4: wave, SIMD, CU, SH, SE) and XCC_ID (hwreg 20)
+  const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+  const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xffu;
+  stamp_val(6, ((unsigned long long)path << 40) | ((unsigned long long)xcc << 32) | hw);
+}
+#else
+__device__ __forceinline__ void stamp_val(int, unsigned long long) {}
+__device__ __forceinline__ void stamp(int) {}
+__device__ __forceinline__ void stamp_path(int) {}
+#endif
 
 // 2^y clamped to [0, 1]: folds into v_exp_f32's clamp, NaN -> 0.
 __device__ __forceinline__ float ex2c(float y) {
@@ -277,53 +302,64 @@ __device__ __forceinline__ void each_chunk_mem(const Row<T, CAP>& R, const Smem<
 }
 
 struct LaneStats {
-  float ml, t1, t2;  // running maximum, two largest chunk maxima
-  int j1;            // chunk holding t1
+  float ml, t1, t2;  // running maximum, two largest chunk-pair maxima
+  int j1;            // chunk pair holding t1 (chunks 2 j1 and 2 j1 + 1)
   double S;          // mass relative to ml
 };
 
-// The pass over the lane's chunks (all loads already issued): running maximum,
-// masses rescaled to it, two largest chunk maxima, chunk-maximum bounds to LDS.
+// The pass over the lane's chunks, two at a time (loads already issued):
+// running maximum, masses rescaled to it, the two largest chunk-pair maxima
+// (distinct elements), chunk-maximum bounds to LDS.  The running maximum, its
+// rescaling and the pair bookkeeping happen once per 16-byte chunk pair.
 // NANIGN: NaN elements are ignored (a second pass for rows holding NaN);
 // otherwise NaN propagates into the maximum and marks the row for that pass.
 template <bool NANIGN, typename T, int CAP, int NW>
 __device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP, NW>& S) {
   constexpr int EPV = QE<T>::EPV;
+  static_assert(CAP % 2 == 0, "chunks are taken in pairs");
   LaneStats s{-INFINITY, -INFINITY, -INFINITY, 0, 0.0};
-  uint32_t pk = 0;
 #pragma unroll
-  for (int j = 0; j < CAP; ++j) {
-    float x[EPV];
+  for (int j = 0; j < CAP; j += 2) {
+    float x[2 * EPV];
     // NANIGN (rare rows holding NaN): chunks re-read from memory, so this pass
     // adds no register pressure to the register-resident row
-    QE<T>::unpack(NANIGN ? R.load(j) : R.d[j], x);
+    QE<T>::unpack(NANIGN ? R.load(j) : R.d[j], *reinterpret_cast<float(*)[EPV]>(&x[0]));
     if constexpr (!NANIGN) R.roll(j);
-    float cm = x[0];
+    QE<T>::unpack(NANIGN ? R.load(j + 1) : R.d[j + 1], *reinterpret_cast<float(*)[EPV]>(&x[EPV]));
+    if constexpr (!NANIGN) R.roll(j + 1);
+    float cm0 = x[0], cm1 = x[EPV];
 #pragma unroll
-    for (int i = 1; i < EPV; ++i) cm = NANIGN ? fmaxf(cm, x[i]) : fmx(cm, x[i]);
-    const float mn = NANIGN ? fmaxf(s.ml, cm) : fmx(s.ml, cm);
+    for (int i = 1; i < EPV; ++i) {
+      cm0 = NANIGN ? fmaxf(cm0, x[i]) : fmx(cm0, x[i]);
+      cm1 = NANIGN ? fmaxf(cm1, x[EPV + i]) : fmx(cm1, x[EPV + i]);
+    }
+    const float cp = NANIGN ? fmaxf(cm0, cm1) : fmx(cm0, cm1);
+    const float mn = NANIGN ? fmaxf(s.ml, cp) : fmx(s.ml, cp);
     const float f = ex2c((s.ml - mn) * c);
-    // masses in two halves of EPV/2 (fewer values live at once)
-    float e[EPV / 2];
+    // masses in quarters of the pair (fewer values live at once)
+    float cs;
 #pragma unroll
-    for (int i = 0; i < EPV / 2; ++i) e[i] = ex2c((x[i] - mn) * c);
-    float cs = tree_sum(e);
-    asm volatile("" : "+v"(cs));
+    for (int h = 0; h < 4; ++h) {
+      float e[EPV / 2];
 #pragma unroll
-    for (int i = 0; i < EPV / 2; ++i) e[i] = ex2c((x[EPV / 2 + i] - mn) * c);
-    cs += tree_sum(e);
+      for (int i = 0; i < EPV / 2; ++i) e[i] = ex2c((x[h * (EPV / 2) + i] - mn) * c);
+      cs = h ? cs + tree_sum(e) : tree_sum(e);
+      asm volatile("" : "+v"(cs));
+    }
     s.S = __builtin_fma(s.S, (double)f, (double)cs);
     s.ml = mn;
-    const float ct = NANIGN ? (cm == cm ? cm : -INFINITY) : cm;
+    const float ct = NANIGN ? (cp == cp ? cp : -INFINITY) : cp;
     s.t2 = __builtin_amdgcn_fmed3f(s.t1, s.t2, ct);
-    s.j1 = ct > s.t1 ? j : s.j1;
+    s.j1 = ct > s.t1 ? (j >> 1) : s.j1;
     s.t1 = fmx(s.t1, ct);
-    const uint32_t h = bf16_up(cm);
-    if (j & 1) S.cm[threadIdx.x][j >> 1] = pk | (h << 16);
-    else pk = h;
+    // (a bf16 chunk maximum is its own bound)
+    if constexpr (std::is_same<T, bf16_t>::value)
+      S.cm[threadIdx.x][j >> 1] = (__float_as_uint(cm0) >> 16) | (__float_as_uint(cm1) & 0xffff0000u);
+    else
+      S.cm[threadIdx.x][j >> 1] = bf16_up(cm0) | (bf16_up(cm1) << 16);
     // materialise the running state here (not sunk to its first use, which
-    // would keep every chunk's operands live), one chunk at a time
-    asm volatile("" : "+v"(s.ml), "+v"(s.t1), "+v"(s.t2), "+v"(s.j1), "+v"(s.S), "+v"(pk));
+    // would keep every chunk's operands live), one pair at a time
+    asm volatile("" : "+v"(s.ml), "+v"(s.t1), "+v"(s.t2), "+v"(s.j1), "+v"(s.S));
     __builtin_amdgcn_sched_barrier(0);
   }
   return s;
@@ -1113,6 +1149,79 @@ __device__ __forceinline__ void window_finish(Smem<CAP, NW>& S, int nw, const in
 }
 
 
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+  return (uint32_t)wave_max_i((int)(v ^ 0x80000000u)) ^ 0x80000000u;
+}
+
+// Finish of a window of at most 64 entries by wave 0, one entry per lane in
+// index order.  Each lane writes its (value key, 2^-40 fixed-point mass) to an
+// LDS table, then reads the whole table (broadcast reads): the k-th largest
+// value key is the largest key with at least k entries at or above it, the
+// top-p threshold the largest kept key whose mass at or above it reaches p * Z
+// (ties kept); the inverse CDF is one wave scan over the kept masses.
+template <int CAP, int NW>
+__device__ __forceinline__ void small_finish(Smem<CAP, NW>& S, int n, const int (&cq)[NW], float m, float c, double Z,
+                                             bool kon, int32_t k, bool pon, float p, float u, int32_t* out) {
+  const int lane = threadIdx.x & 63;
+  int w = 0, off = lane, base = 0;
+#pragma unroll
+  for (int g = 1; g < NW; ++g) {
+    base += cq[g - 1];
+    const bool ge = lane >= base;
+    w = ge ? g : w;
+    off = ge ? lane - base : off;
+  }
+  const bool in = lane < n;
+  const uint64_t key = in ? S.seg[w][off] : 0ull;
+  const uint32_t kx = (uint32_t)(key >> 32);
+  const uint32_t idx = 0xffffffffu - (uint32_t)(key & 0xffffffffu);
+  const float e = in ? ex2c((okey_inv(kx) - m) * c) : 0.0f;
+  const double f = (double)fix40(e);  // exact (< 2^40), and so are sums of 64 of them
+  // the table: entry j = (value key, mass) at fmass[2 j], fmass[2 j + 1]
+  unsigned long long* tab = S.fmass;
+  if (in) {
+    tab[2 * lane] = (unsigned long long)kx;
+    tab[2 * lane + 1] = (unsigned long long)__double_as_longlong(f);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's table writes are done
+  __builtin_amdgcn_wave_barrier();
+  uint32_t thr = 0u;  // keep entries with value key >= thr
+  double ZK = Z;
+  if (kon) {
+    int cnt = 0;
+#pragma unroll 8
+    for (int j = 0; j < n; ++j) cnt += (uint32_t)tab[2 * j] >= kx ? 1 : 0;
+    const int kk = k < n ? k : n;
+    thr = wave_max_u(in && cnt >= kk ? kx : 0u);
+    ZK = wave_sum(in && kx >= thr ? (double)e : 0.0);
+  }
+  if (pon) {
+    const double target = (double)p * ZK * kFix;
+    double A = 0.0;
+#pragma unroll 8
+    for (int j = 0; j < n; ++j) {
+      const uint32_t kj = (uint32_t)tab[2 * j];
+      const double fj = __longlong_as_double((long long)tab[2 * j + 1]);
+      A += (kj >= kx && kj >= thr) ? fj : 0.0;
+    }
+    thr = max(thr, wave_max_u(in && kx >= thr && A >= target ? kx : 0u));
+  }
+  // inverse CDF in vocabulary (lane) order over the kept entries
+  const bool kept = in && kx >= thr;
+  const double ek = kept ? (double)e : 0.0;
+  const double inc = wave_incl_scan(ek, lane);
+  const double U = (double)uni(u) * readlane_d(inc, 63);
+  const uint64_t hit = __ballot(ek > 0.0 && inc > U);
+  int src;
+  if (hit) {
+    src = __ffsll((unsigned long long)hit) - 1;
+  } else {  // rounding (u ~ 1): the last kept entry with mass, else the last kept
+    const uint64_t pos = __ballot(ek > 0.0), any = __ballot(kept);
+    src = pos ? 63 - __clzll((long long)pos) : (any ? 63 - __clzll((long long)any) : 0);
+  }
+  if (lane == src) *out = (int32_t)idx;
+}
+
 // Row statistics after the pass, published per wave before barrier 1.
 template <typename T, int CAP, int NW>
 __device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, bool pon, Smem<CAP, NW>& S) {
@@ -1156,6 +1265,7 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(wave
 void quad_sample_kernel(SampleParams P) {
   constexpr int EPV = QE<T>::EPV;
   __shared__ Smem<CAP, NW> S;
+  stamp(0);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   int64_t nrows = P.B_out;
   if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
@@ -1180,6 +1290,7 @@ void quad_sample_kernel(SampleParams P) {
   Row<T, CAP> R;
   R.init(P.logits, r, P.ld, (uint32_t)P.V);
   R.fetch();
+  stamp(7);
   const float Tr = __uint_as_float(uni(aT));
   const float u = __uint_as_float(uni(aU));
   const int32_t k = (int32_t)uni(aK);
@@ -1191,7 +1302,9 @@ void quad_sample_kernel(SampleParams P) {
   if (tvalid) {
     if (kon || pon) S.wh[wid][lane] = S.wh[wid][lane + kWave] = 0u;  // this wave's histogram (a wave's LDS ops stay in order)
     publish<T, CAP>(lane_pass<false>(R, c, S), c, kon, pon, S);
+    stamp(1);
     __syncthreads();
+    stamp(2);
     m = S.wmax[0];
 #pragma unroll
     for (int q = 1; q < NW; ++q) m = fmx(m, S.wmax[q]);
@@ -1208,12 +1321,16 @@ void quad_sample_kernel(SampleParams P) {
   }
   if (!tvalid || !(m > -INFINITY) || !(m < INFINITY)) {
     row_argmax<true, NW>(R, S, out);
+    stamp(5);
+    stamp_path(kPathArgmax);
     return;
   }
   __builtin_amdgcn_s_setprio(2);
   m = uni(m);
   if (!kon && !pon) {
     walk_cols(R, S, m, c, u, [&](float x) { return ex2c((x - m) * c); }, out);
+    stamp(5);
+    stamp_path(kPathWalk);
     return;
   }
   // ---- top-k / top-p: floor from the merged histograms (row bin b gathers
@@ -1262,6 +1379,7 @@ void quad_sample_kernel(SampleParams P) {
     }
     bstar = lb < 0 ? -1 : 2 * lb + hb;
   }
+  stamp(3);
   float Lm = -INFINITY;
   if (bstar >= 0) {
     Lm = -0.25f * (float)(bstar + 1) - 0x1p-8f;
@@ -1270,12 +1388,17 @@ void quad_sample_kernel(SampleParams P) {
     int run = 0;
     // this lane's chunks whose maximum bound reaches the floor (all bound
     // words read at once), and the columns where any lane has one
-    // (a lane whose second-largest chunk maximum is below the floor has at
-    // most one such chunk, the one holding its largest; only lanes with more
+    // (a lane whose second-largest chunk-pair maximum is below the floor has
+    // at most the two chunks of its largest pair there; only lanes with more
     // read their chunk bounds)
     const v4u lt = S.lt[threadIdx.x];
     const bool t2in = (__uint_as_float(lt.y) - m) * c >= Lm;
-    uint32_t hm = (__uint_as_float(lt.x) - m) * c >= Lm ? (1u << lt.z) : 0u;
+    uint32_t hm = 0u;
+    if ((__uint_as_float(lt.x) - m) * c >= Lm) {  // the chunks of the largest pair whose bounds reach the floor
+      const uint32_t w = S.cm[threadIdx.x][lt.z];
+      hm = (((__uint_as_float(w << 16) - m) * c >= Lm ? 1u : 0u) |
+            ((__uint_as_float(w & 0xffff0000u) - m) * c >= Lm ? 2u : 0u)) << (2 * lt.z);
+    }
     if (__ballot(t2in) && t2in) {
       hm = 0u;
 #pragma unroll
@@ -1292,18 +1415,31 @@ void quad_sample_kernel(SampleParams P) {
     v4u* stg = S.stg[wid];
     uint32_t* meta = S.smeta[wid];
     int ns = 0;
-#pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      if ((cols >> j) & 1u) {
+    if constexpr (streams(CAP)) {
+      // only the occupied columns, in order (a scalar loop over their bits)
+      for (uint32_t cb = cols; cb; cb &= cb - 1u) {
+        const int j = __builtin_ctz(cb);
         const bool hj = (hm >> j) & 1u;
         const uint64_t bj = __ballot(hj);
         const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
-        if (hj && slot < stg_cap(NW)) {
-          if constexpr (!streams(CAP)) stg[slot] = R.d[j];
-          meta[slot] = (uint32_t)(j * kWave + lane);
-        }
+        if (hj && slot < stg_cap(NW)) meta[slot] = (uint32_t)(j * kWave + lane);
         ns += (int)__popcll(bj);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CAP; ++j) {
+        if ((cols >> j) & 1u) {
+          const bool hj = (hm >> j) & 1u;
+          const uint64_t bj = __ballot(hj);
+          const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
+          if (hj && slot < stg_cap(NW)) {
+            stg[slot] = R.d[j];
+            meta[slot] = (uint32_t)(j * kWave + lane);
+          }
+          ns += (int)__popcll(bj);
+        }
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's staging writes are done
@@ -1353,6 +1489,7 @@ void quad_sample_kernel(SampleParams P) {
     if (lane == 0) S.cnt[wid] = run;
   }
   __syncthreads();
+  stamp(4);
   if (bstar >= 0) {
     int cq[NW], nw = 0;
     bool ovf = false;
@@ -1362,14 +1499,28 @@ void quad_sample_kernel(SampleParams P) {
       nw += cq[q];
       ovf = ovf || cq[q] > seg_cap(NW);
     }
+    if (!ovf && nw >= 1 && nw <= kWave) {
+      if (wid == 0) small_finish(S, nw, cq, m, c, (!kon && pon) ? S.rz : 0.0, kon, k, pon, p, u, out);
+      stamp(5);
+      stamp_path(kPathSmall);
+      return;
+    }
     if (!ovf && nw <= kWin) {
       if (wid == 0) window_finish(S, nw, cq, m, c, (!kon && pon) ? S.rz : 0.0, kon, k, pon, p, u, out);
+      stamp(5);
+      stamp_path(kPathWindow);
       return;
     }
   }
   const double Zr = wave_total<NW>([&](int q) { return wave_mass(S, q, m, c); });
-  if (!kon && row_topp_fast(R, S, m, c, Zr, p, bstar >= 0 ? Lm : -INFINITY, u, P.V, out)) return;
+  if (!kon && row_topp_fast(R, S, m, c, Zr, p, bstar >= 0 ? Lm : -INFINITY, u, P.V, out)) {
+    stamp(5);
+    stamp_path(kPathTopp);
+    return;
+  }
   row_exact(R, S, m, c, Zr, kon, k, pon, p, bstar >= 0 ? Lm : -INFINITY, u, out);
+  stamp(5);
+  stamp_path(kPathExact);
 }
 
 // All-greedy batch: torch.argmax per row.
@@ -1437,6 +1588,16 @@ static bool launch_dtype(const SampleParams& P, bool greedy, hipStream_t st) {
 }
 
 }  // namespace quad
+
+#ifdef LSG_PHASE_STAMPS
+// Copy of the phase stamps (profiling build only): kStampRows x kStampSlots
+// 64-bit words.
+extern "C" int lsg_phase_stamps_read(void* dst, size_t bytes) {
+  const size_t n = sizeof(quad::g_phase_stamps);
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(quad::g_phase_stamps), bytes < n ? bytes : n, 0,
+                                  hipMemcpyDeviceToHost);
+}
+#endif
 
 bool quad_sample_launch(const SampleParams& P, int dtype, bool greedy, bool vec, hipStream_t st) {
   if (!vec) return false;
