@@ -18,9 +18,10 @@ struct SampleParams {
   int32_t* out;
 };
 
-// Launches the four-wave row sampler (sample_quad.hip) when the row shape is one
-// it holds in registers (16-byte aligned rows of exactly 256 * CAP chunks);
-// returns false, launching nothing, otherwise.
+// Launches the streamed row sampler (sample_quad.hip) when the batch has more
+// rows than the device has compute units and the row shape is one it serves
+// (16-byte aligned rows of exactly 256 * CAP chunks); returns false, launching
+// nothing, otherwise.
 bool quad_sample_launch(const SampleParams& P, int dtype, bool greedy, bool vec, hipStream_t st);
 
 }  // namespace lsg

@@ -1,36 +1,40 @@
-// Token sampling with one four-wave workgroup per row (the row held in registers).
+// Token sampling with one workgroup per row, the row streamed through registers.
 //
 // Replaces, for the decode token path of Loop-SGLang:
 //   Sampler.sample            python/loopsgl/model_executor/sample.py:107-112
 //   torch.argmax (greedy)     sample.py:110-111 (+ int32 cast, model_runner.py:279-280)
 //   sample_impl -> flashinfer softmax / *_sampling_from_probs   sample.py:60-81
-// for rows of exactly 256 * CAP 16-byte chunks (V = 65536 or 49152 for bf16/fp16,
-// 32768 or 24576 for fp32); sample.hip serves every other shape with the same
-// semantics:
+// for batches of more rows than compute units whose rows are exactly 256 * CAP
+// 16-byte chunks (V = 65536 or 49152 for bf16/fp16, 32768 or 24576 for fp32;
+// fp32 rows of 65536 take eight waves); sample.hip serves every other case with
+// the same semantics:
 //   T <= 0 or non-finite, or max x non-finite  -> id = argmax (torch rules)
 //   m = max x (NaN ignored), e_i = 2^((x_i - m) * log2(e)/T)
 //   K = {x >= k-th largest x} if 1 <= k < V            (ties kept)
 //   P = {x in K : x >= tau}, tau = largest x with mass(x >= tau) >= p * mass(K)
 //   id = first index j in P (ascending) with cumsum_P(e)[j] > u * sum_P(e)
 //
-// Structure (one row per 256-thread workgroup, three resident per CU):
-//   * every lane issues all of its CAP nontemporal 128-bit loads at once; wave w
-//     owns chunks [w*CAP*64, (w+1)*CAP*64), its j-th load reads the 64 chunks
-//     (w*CAP + j)*64 + lane (1 KiB contiguous), so index order is (wave, j, lane,
-//     element);
-//   * one pass over the chunks as they arrive: a running maximum per lane with
+// Structure (four four-wave rows resident per compute unit, so a batch of 1024
+// rows runs in one generation):
+//   * each lane streams its CAP nontemporal 128-bit loads through a rolling
+//     window of 16; wave w owns chunks [w*CAP*64, (w+1)*CAP*64), its j-th load
+//     reads the 64 chunks (w*CAP + j)*64 + lane (1 KiB contiguous), so index
+//     order is (wave, j, lane, element);
+//   * one pass over chunk pairs as they arrive: a running maximum per lane with
 //     the masses rescaled whenever it rises (e = 2^((x - max) c) is exact near
-//     the maximum, whatever the data), the lane's two largest chunk maxima and a
+//     the maximum, whatever the data), the lane's two largest pair maxima and a
 //     16-bit upper bound of every chunk maximum (to LDS);
-//   * barrier 1: the row maximum and normaliser from four wave summaries;
-//     unfiltered rows walk the inverse CDF right away (crossing wave, lane, chunk,
-//     element);
-//   * top-k / top-p rows: a histogram of the lanes' two largest chunk maxima
-//     (distinct elements) bounds the threshold from below; every wave stages its
-//     elements above the bound in index order; barrier 2; one wave finishes the
-//     window (<= 256 entries) with a 1/8-binary-order histogram, an exact
-//     resolution inside the crossing bin and the walk.  Larger windows take an
-//     exact radix refinement over the row.
+//   * barrier 1: the row maximum and normaliser from the wave summaries;
+//     unfiltered rows walk the inverse CDF right away (crossing wave, chunk,
+//     lane, element; chunks re-read from memory);
+//   * top-k / top-p rows: a histogram of the lanes' two largest pair maxima
+//     (distinct elements) bounds the threshold from below; every wave lists its
+//     chunks whose bounds reach it and gathers them from memory, staging the
+//     elements above the bound in index order; barrier 2; one wave finishes
+//     the window: at most 64 entries from an LDS table (counts and masses at or
+//     above each entry, a scan for the draw), up to 512 with a 1/8-binary-order
+//     histogram and an exact resolution inside the crossing bin.  Larger
+//     windows take the two-pass exact top-p or the exact radix refinement.
 // Sums above the chunk level are float64; window masses are 2^-40 fixed point,
 // so the threshold sums are exact and independent of atomic order.
 #include <type_traits>
@@ -50,16 +54,12 @@ constexpr int stg_cap(int nw) { return 512 / nw; }    // candidate chunks staged
 // exact top-p candidates per wave (four-wave rows: 1024, so that four rows fit
 // one compute unit's LDS)
 constexpr int cand_cap(int nw) { return nw == 4 ? 256 : 1536 / nw; }
-// Loads in flight per lane during the pass.  Rows of more than 16 chunks per
-// lane stream through a rolling window of 16 (the chunks are not kept: later
-// phases re-read the few they need), so that four four-wave rows, or two
-// eight-wave rows, are resident per compute unit; shorter rows are loaded whole
-// and stay in registers.
-constexpr int load_window(int cap) { return cap > 16 ? 16 : cap; }
-constexpr bool streams(int cap) { return load_window(cap) < cap; }
-// Waves per SIMD the kernels are compiled for (128 registers, or 168 for the
-// twelve-wave row of 8 chunks per lane, one row per compute unit).
-constexpr int waves_per_eu(int nw) { return nw == 12 ? 3 : 4; }
+// Loads in flight per lane during the pass: the row streams through a rolling
+// window of 16 chunks per lane (the chunks are not kept: later phases re-read
+// the few they need), so that four four-wave rows, or two eight-wave rows, are
+// resident per compute unit (128 registers, four waves per SIMD).
+constexpr int kLoadWindow = 16;
+constexpr int kWavesPerEU = 4;
 constexpr int kHB = 128;          // coarse histogram: bins of 1/4 binary order over y in [-32, 0]
 constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order over y in [-32, 0]
 constexpr int kWin = 512;         // window finished by one wave
@@ -182,9 +182,7 @@ struct Smem {
       uint64_t seg[NW][seg_cap(NW)];                    // window entries per wave, index order
       unsigned long long fmass[kFB];              // fine histogram: masses (2^-40 fixed point)
       uint32_t fcnt[kFB];                         // fine histogram: counts
-      v4u stg[NW][streams(CAP) ? 1 : stg_cap(NW)];      // staged candidate chunks per wave, (column, lane) order
-                                                        //   (streamed rows re-read them instead)
-      uint32_t smeta[NW][stg_cap(NW)];                  // their column * 64 + lane
+      uint32_t smeta[NW][stg_cap(NW)];                  // candidate chunks per wave: column * 64 + lane
     };
     struct {                                      // exact refinement and its inverse CDF
       unsigned long long rb[4][kRB + 1];          // refinement bins, four copies by lane
@@ -234,14 +232,15 @@ struct Row {
   __device__ __forceinline__ void issue(int j) {
     d[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(c0 * 16u), j * kWave * 16, kNonTemporal);
   }
-  // The first load_window(CAP) loads; the pass issues the rest as it goes.
+  // The first kLoadWindow loads; the pass issues the rest as it goes.
   __device__ __forceinline__ void fetch() {
+    static_assert(CAP > kLoadWindow, "rows stream through the load window");
 #pragma unroll
-    for (int j = 0; j < load_window(CAP); ++j) issue(j);
+    for (int j = 0; j < kLoadWindow; ++j) issue(j);
   }
   // After chunk j is unpacked: the load that takes its place in the window.
   __device__ __forceinline__ void roll(int j) {
-    if (j + load_window(CAP) < CAP) issue(j + load_window(CAP));
+    if (j + kLoadWindow < CAP) issue(j + kLoadWindow);
   }
   // Chunk `chunk` of the row re-read from memory (cold paths: the register
   // copy is then no longer needed, so those paths add no register pressure).
@@ -267,25 +266,11 @@ __device__ __forceinline__ float cm_at(const Smem<CAP, NW>& S, int j) {
 }
 
 // f(j, chunk, keep) over this lane's chunks re-read from memory, eight loads
-// in flight at a time (rows of at most eight chunks per lane are read from
-// their register copy); chunks whose maximum bound fails keep() in every lane
-// of the wave are skipped (and not loaded by the lanes that fail it).
+// in flight at a time; chunks whose maximum bound fails keep() in every lane of
+// the wave are skipped (and not loaded by the lanes that fail it).
 template <typename T, int CAP, class K, class F, int NW>
 __device__ __forceinline__ void each_chunk_mem(const Row<T, CAP>& R, const Smem<CAP, NW>& S, K&& keep, F&& f) {
   static_assert(CAP % 8 == 0, "chunks are re-read in groups of eight");
-  if constexpr (CAP <= 8 && (NW <= 12 || std::is_same<T, bf16_t>::value)) {
-    // a short row stays in registers: no re-read (values unpacked by an
-    // earlier pass are recomputed, not kept live); sixteen-wave rows other
-    // than bf16 keep re-reading (their 128-register budget)
-    R.launder();
-#pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      const bool kp = keep(cm_at(S, j));
-      if (__ballot(kp)) f(j, R.d[j], kp);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return;
-  }
 #pragma unroll 1
   for (int jb = 0; jb < CAP; jb += 8) {
     v4u v[8];
@@ -366,12 +351,12 @@ __device__ __forceinline__ LaneStats lane_pass(Row<T, CAP>& R, float c, Smem<CAP
 }
 
 // Maximum pass only (argmax): NaN-propagating lane maximum and the first chunk
-// at which it was reached (for NaN: the first chunk holding a NaN).  A streamed
-// row keeps a copy of that chunk in *best as it goes.
+// at which it was reached (for NaN: the first chunk holding a NaN).  Streaming
+// (!MEM), the lane keeps a copy of that chunk in *best as it goes.
 template <bool MEM, typename T, int CAP>
 __device__ __forceinline__ float lane_max(Row<T, CAP>& R, int* fj, v4u* best) {
   constexpr int EPV = QE<T>::EPV;
-  constexpr bool ST = !MEM && streams(CAP);
+  constexpr bool ST = !MEM;
   float ml = -INFINITY;
   int f = 0;
   v4u bv = {0u, 0u, 0u, 0u};
@@ -434,23 +419,8 @@ __device__ __forceinline__ void row_argmax(Row<T, CAP>& R, SM& S, int32_t* out) 
   const float m = uni(mw);
   const bool isn = m != m;
   const bool cand = isn ? (ml != ml) : (ml == m);
-  // the chunk where this lane first reached the maximum (from registers:
-  // masked ORs, no dynamic register indexing)
-  v4u v = {0u, 0u, 0u, 0u};
-  if constexpr (MEM) {
-    v = R.load(fj);
-  } else if constexpr (streams(CAP)) {
-    v = best;
-  } else {
-#pragma unroll
-    for (int j = 0; j < CAP; ++j) {
-      const uint32_t mk = 0u - (uint32_t)(fj == j);
-      v.x |= R.d[j].x & mk;
-      v.y |= R.d[j].y & mk;
-      v.z |= R.d[j].z & mk;
-      v.w |= R.d[j].w & mk;
-    }
-  }
+  // the chunk where this lane first reached the maximum
+  const v4u v = MEM ? R.load(fj) : best;
   float x[EPV];
   QE<T>::unpack(v, x);
   int first = 0x7fffffff;
@@ -1261,7 +1231,7 @@ __device__ __forceinline__ void publish(const LaneStats& s, float c, bool kon, b
 }
 
 template <typename T, int CAP, int NW>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(waves_per_eu(NW))))
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEU)))
 void quad_sample_kernel(SampleParams P) {
   constexpr int EPV = QE<T>::EPV;
   __shared__ Smem<CAP, NW> S;
@@ -1409,62 +1379,41 @@ void quad_sample_kernel(SampleParams P) {
       }
     }
     const uint32_t cols = uni(wave_or(hm));
-    // A: the lanes holding a candidate chunk list it (and, for a row held in
-    // registers, copy it) in this wave's staging area, column by column (slots
-    // in (column, lane) = index order)
-    v4u* stg = S.stg[wid];
+    // A: the lanes holding a candidate chunk list it in this wave's staging
+    // area, over the occupied columns in order (a scalar loop over their bits;
+    // slots in (column, lane) = index order)
     uint32_t* meta = S.smeta[wid];
     int ns = 0;
-    if constexpr (streams(CAP)) {
-      // only the occupied columns, in order (a scalar loop over their bits)
-      for (uint32_t cb = cols; cb; cb &= cb - 1u) {
-        const int j = __builtin_ctz(cb);
-        const bool hj = (hm >> j) & 1u;
-        const uint64_t bj = __ballot(hj);
-        const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
-        if (hj && slot < stg_cap(NW)) meta[slot] = (uint32_t)(j * kWave + lane);
-        ns += (int)__popcll(bj);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < CAP; ++j) {
-        if ((cols >> j) & 1u) {
-          const bool hj = (hm >> j) & 1u;
-          const uint64_t bj = __ballot(hj);
-          const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
-          if (hj && slot < stg_cap(NW)) {
-            stg[slot] = R.d[j];
-            meta[slot] = (uint32_t)(j * kWave + lane);
-          }
-          ns += (int)__popcll(bj);
-        }
-      }
+    for (uint32_t cb = cols; cb; cb &= cb - 1u) {
+      const int j = __builtin_ctz(cb);
+      const bool hj = (hm >> j) & 1u;
+      const uint64_t bj = __ballot(hj);
+      const int slot = ns + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bj >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bj, 0u));
+      if (hj && slot < stg_cap(NW)) meta[slot] = (uint32_t)(j * kWave + lane);
+      ns += (int)__popcll(bj);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's staging writes are done
     __builtin_amdgcn_wave_barrier();
-    // B: lane i takes staged chunks i and i + 64 and writes their elements
-    // above the floor (slot order is index order); a streamed row gathers those
-    // chunks from memory, all rounds' loads at once
+    // B: lane i gathers staged chunks i and i + 64 from memory (all rounds'
+    // loads at once) and writes their elements above the floor (slot order is
+    // index order)
     if (ns <= stg_cap(NW)) {
       constexpr int NR = (stg_cap(NW) + kWave - 1) / kWave;
       v4u gv[NR];
-      if constexpr (streams(CAP)) {
 #pragma unroll
-        for (int rr = 0; rr < NR; ++rr) {
-          const int sl = rr * kWave + lane;
-          const uint32_t mt = meta[sl < ns ? sl : 0];
-          const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);
-          gv[rr] = sl < ns ? R.load_at(ci) : v4u{0u, 0u, 0u, 0u};
-        }
+      for (int rr = 0; rr < NR; ++rr) {
+        const int sl = rr * kWave + lane;
+        const uint32_t mt = meta[sl < ns ? sl : 0];
+        const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);
+        gv[rr] = sl < ns ? R.load_at(ci) : v4u{0u, 0u, 0u, 0u};
       }
 #pragma unroll
       for (int rr = 0; rr < NR; ++rr) {
         const int r0 = rr * kWave;
         if (r0 >= ns) break;
         const bool act = r0 + lane < ns;
-        const v4u v = streams(CAP) ? gv[rr] : stg[act ? r0 + lane : 0];
+        const v4u v = gv[rr];
         const uint32_t mt = meta[act ? r0 + lane : 0];
         const uint32_t ci = ((uint32_t)wid * CAP + (mt >> 6)) * kWave + (mt & 63u);  // chunk index in the row
         float x[EPV];
@@ -1525,7 +1474,7 @@ void quad_sample_kernel(SampleParams P) {
 
 // All-greedy batch: torch.argmax per row.
 template <typename T, int CAP, int NW>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(waves_per_eu(NW))))
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(kWavesPerEU)))
 void quad_greedy_kernel(SampleParams P) {
   __shared__ GSmem<NW> S;
   int64_t nrows = P.B_out;
@@ -1551,32 +1500,21 @@ static void launch(const SampleParams& P, bool greedy, hipStream_t st) {
     hipLaunchKernelGGL((quad_sample_kernel<T, CAP, NW>), dim3((unsigned)P.B_out), dim3(NW * kWave), 0, st, P);
 }
 
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
-// Row shapes held in registers: 4 waves x 32 or 24 chunks per lane (three rows
-// per compute unit); when the batch has no more rows than compute units, 16
-// or 12 waves x 8 chunks (one row per compute unit, all of its SIMDs busy);
-// fp32 rows of 65536 as 8 waves x 32 chunks (one row per compute unit).
+// Row shapes this file serves: 4 waves x 32 or 24 chunks per lane (four rows
+// per compute unit), and fp32 rows of 65536 as 8 waves x 32 chunks (two rows
+// per compute unit).  Batches with no more rows than compute units are left to
+// sample.hip's sixteen-wave rows (one row per compute unit, all of its SIMDs
+// busy), which finish such batches sooner.
 template <typename T>
 static bool launch_dtype(const SampleParams& P, bool greedy, hipStream_t st) {
   constexpr int EPV = QE<T>::EPV;
   if (P.V % EPV != 0) return false;
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess)
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (P.B_out <= (int64_t)cus) return false;
   const int64_t NV = P.V / EPV;
-  const bool small = P.B_out <= (int64_t)device_cus();
-  if (NV == 16 * kWave * 8 && small) launch<T, 8, 16>(P, greedy, st);
-  else if (NV == 12 * kWave * 8 && small) launch<T, 8, 12>(P, greedy, st);
-  else if (NV == 4 * kWave * 32) launch<T, 32, 4>(P, greedy, st);
+  if (NV == 4 * kWave * 32) launch<T, 32, 4>(P, greedy, st);
   else if (NV == 4 * kWave * 24) launch<T, 24, 4>(P, greedy, st);
   else if constexpr (sizeof(T) == 4) {
     if (NV == 8 * kWave * 32) launch<T, 32, 8>(P, greedy, st);

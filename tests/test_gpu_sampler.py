@@ -300,6 +300,36 @@ def test_large_batches(lsg, orc, dev, dtype, V):
     assert torch.equal(ids.long(), torch.argmax(x, -1))
 
 
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 65536), (torch.float16, 49152), (torch.float32, 32768),
+                                     (torch.float32, 65536)])
+def test_streamed_rows_edge_cases(lsg, orc, dev, dtype, V):
+    """B=320 (more rows than compute units: the streamed row kernel): the
+    argmax edge cases of the small-batch test (NaN, all -inf, +inf, ties, -0,
+    constant rows) in greedy and sampling modes, next to NaN-holding rows."""
+    g = torch.Generator(device=dev).manual_seed(V + 31)
+    B = 320
+    x = (torch.randn(B, V, generator=g, device=dev) * 2).to(dtype)
+    x[0, V // 3] = float("nan")
+    x[1, :] = 0.0
+    x[1, V // 2] = -0.0
+    x[2, V - 1] = float("inf")
+    x[3, :] = float("-inf")
+    x[4, :] = float("nan")
+    x[5, 3] = 9.0
+    x[5, V - 2] = 9.0
+    x[6, :] = 1.0
+    x[7, V - 1] = float("inf")
+    x[7, 1] = float("nan")
+    x[8, ::5] = float("nan")
+    x[10, :] = float("-inf")
+    x[10, 12345] = -3.0
+    ids = lsg.sample_rows(x, None, None, None, None).cpu().numpy()
+    assert np.array_equal(ids, torch.argmax(x, dim=-1).to(torch.int32).cpu().numpy())
+    T, K, P, U = _mixed_params(B, V, g, dev)
+    ids, _, _ = check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.05)
+    assert ids[8] % 5 != 0 and ids[10] == 12345
+
+
 def test_large_gather_and_count(lsg, orc, dev):
     """Large batch with row_idx (invalid entries -> -1) and a device row count
     below B_out: rows past the count stay untouched."""
