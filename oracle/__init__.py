@@ -52,7 +52,7 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(LIB_PATH)
         P, I64, I32, F, D = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_double
         L.orc_argmax.argtypes = [P, ctypes.c_int, I64, I64, I64, P, ctypes.c_int]
-        L.orc_sample.argtypes = [P, ctypes.c_int, I64, I64, I64, P, P, P, P, P, P, D, ctypes.c_int]
+        L.orc_sample.argtypes = [P, ctypes.c_int, I64, I64, I64, P, P, P, P, P, P, D, ctypes.c_int, P]
         L.orc_exit_gate.argtypes = [P, ctypes.c_int, I64, I64, I64, P, P, P, P, I32, F, I32, I32,
                                     I32, P, P, P, P, P, P, P]
         L.orc_cumulative_exit_probability.argtypes = [P, P, I64, P]
@@ -90,8 +90,11 @@ def argmax(logits: np.ndarray, dtype: int | None = None, nthreads: int = 0) -> n
 
 
 def sample(logits: np.ndarray, temperatures, top_k, top_p, uniforms, dtype: int | None = None,
-           tol: float = AMB_TOL, nthreads: int = 0):
-    """Non-greedy sampling (S2-S5). Returns (ids int32[B], amb uint8[B]).
+           tol: float = AMB_TOL, nthreads: int = 0, with_alt: bool = False):
+    """Non-greedy sampling (S2-S5). Returns (ids int32[B], amb uint8[B]), and with
+    ``with_alt`` also alt int32[B]: for rows whose top-p mass is ambiguous (amb
+    bit 1), the draw from the other kept set a float evaluation can produce
+    (amb bit 2: that draw's CDF is itself within tol of u); elsewhere alt = ids.
 
     ``temperatures is None`` selects the all-greedy branch (argmax), matching
     ``Sampler.sample`` (sample.py:110).  ``top_k``/``top_p``/``uniforms`` may be None.
@@ -101,9 +104,10 @@ def sample(logits: np.ndarray, temperatures, top_k, top_p, uniforms, dtype: int 
     T, K, Pp, U = f(temperatures, np.float32), f(top_k, np.int32), f(top_p, np.float32), f(uniforms, np.float32)
     out = np.empty(B, np.int32)
     amb = np.zeros(B, np.uint8)
+    alt = np.empty(B, np.int32)
     lib().orc_sample(_ptr(logits), _dtype_code(logits, dtype), B, V, ld, _ptr(T), _ptr(K), _ptr(Pp),
-                     _ptr(U), _ptr(out), _ptr(amb), tol, nthreads)
-    return out, amb
+                     _ptr(U), _ptr(out), _ptr(amb), tol, nthreads, _ptr(alt))
+    return (out, amb, alt) if with_alt else (out, amb)
 
 
 def exit_gate(h: np.ndarray, w: np.ndarray, bias, F_prev, loop_step, tau: float,

@@ -191,7 +191,13 @@ static int cmp_asc_i64(const void* a, const void* b) {
  *          if p < 1, else K                        (S4, ties kept)
  *   id   = min{j in P : sum_{i in P, i<=j} e_i > u * sum_P e}   (S5)
  * amb bit 0: the CDF at the chosen boundary lies within tol of u.
- * amb bit 1: the top-p mass at tau lies within tol of p.
+ * amb bit 1: the top-p mass at tau lies within tol of p.  The row then also
+ *            has an alternative id: the draw from the other kept set a float
+ *            evaluation of the same comparison can produce (the next tie group
+ *            included when the crossing group's mass reaches p*Z_K by less than
+ *            tol, the crossing group left out when the mass above it falls short
+ *            of p*Z_K by less than tol).
+ * amb bit 2: that alternative draw's CDF lies within tol of u.
  * ------------------------------------------------------------------------ */
 typedef struct {
   uint64_t* keys;
@@ -200,8 +206,33 @@ typedef struct {
   int64_t cap;
 } scratch_t;
 
+/* Inverse CDF over the first nP entries of the descending key order, in
+ * ascending index order (S5); sets `flag` in *amb when the CDF at the chosen
+ * boundary lies within tol of u. */
+static int32_t walk_prefix(scratch_t* s, int64_t nP, float u, double tol, uint8_t* amb, uint8_t flag) {
+  for (int64_t q = 0; q < nP; ++q) s->idx[q] = (int64_t)(0xffffffffu - (uint32_t)s->keys[q]);
+  qsort(s->idx, (size_t)nP, sizeof(int64_t), cmp_asc_i64);
+  double sigma = 0.0;
+  for (int64_t q = 0; q < nP; ++q) sigma += s->e[s->idx[q]];
+  double U = (double)u * sigma, cum = 0.0;
+  int64_t last_pos = -1;
+  for (int64_t q = 0; q < nP; ++q) {
+    double ei = s->e[s->idx[q]];
+    if (ei <= 0.0) continue;
+    double prev = cum;
+    cum += ei;
+    last_pos = q;
+    if (cum > U) {
+      if ((cum - U) < tol * sigma || (U - prev) < tol * sigma) *amb |= flag;
+      return (int32_t)s->idx[q];
+    }
+  }
+  *amb |= flag; /* u >= 1 or rounding: fall back to the last element with mass */
+  return last_pos >= 0 ? (int32_t)s->idx[last_pos] : (int32_t)s->idx[0];
+}
+
 static int32_t sample_row(const void* row, int dtype, int64_t V, float T, int32_t k, float p,
-                          float u, double tol, uint8_t* amb, scratch_t* s) {
+                          float u, double tol, uint8_t* amb, int32_t* alt, scratch_t* s) {
   *amb = 0;
   double m = -INFINITY;
   int any = 0;
@@ -239,7 +270,7 @@ static int32_t sample_row(const void* row, int dtype, int64_t V, float T, int32_
   double ZK = 0.0;
   for (int64_t q = 0; q < nK; ++q) ZK += s->e[0xffffffffu - (uint32_t)s->keys[q]];
 
-  int64_t nP = nK;
+  int64_t nP = nK, nP_alt = nK;
   if (pon) {
     double target = (double)p * ZK, cum = 0.0;
     int64_t q = 0;
@@ -253,8 +284,18 @@ static int32_t sample_row(const void* row, int dtype, int64_t V, float T, int32_
         ++g;
       }
       if (cum >= target) {
-        nP = g;
-        if ((cum - target) < tol * ZK || (target - above) < tol * ZK) *amb |= 2;
+        nP = nP_alt = g;
+        if ((cum - target) < tol * ZK) {  /* alternative: the next tie group kept too */
+          *amb |= 2;
+          if (g < nK) {
+            uint32_t nb = (uint32_t)(s->keys[g] >> 32);
+            nP_alt = g;
+            while (nP_alt < nK && (uint32_t)(s->keys[nP_alt] >> 32) == nb) ++nP_alt;
+          }
+        } else if ((target - above) < tol * ZK) {  /* alternative: this group left out */
+          *amb |= 2;
+          if (q > 0) nP_alt = q;
+        }
         break;
       }
       q = g - 1;
@@ -262,32 +303,16 @@ static int32_t sample_row(const void* row, int dtype, int64_t V, float T, int32_
     if (q >= nK) nP = nK; /* unreachable in exact arithmetic (p < 1) */
   }
 
-  /* Inverse CDF over P in ascending index order. */
-  for (int64_t q = 0; q < nP; ++q) s->idx[q] = (int64_t)(0xffffffffu - (uint32_t)s->keys[q]);
-  qsort(s->idx, (size_t)nP, sizeof(int64_t), cmp_asc_i64);
-  double sigma = 0.0;
-  for (int64_t q = 0; q < nP; ++q) sigma += s->e[s->idx[q]];
-  double U = (double)u * sigma, cum = 0.0;
-  int64_t last_pos = -1;
-  for (int64_t q = 0; q < nP; ++q) {
-    double ei = s->e[s->idx[q]];
-    if (ei <= 0.0) continue;
-    double prev = cum;
-    cum += ei;
-    last_pos = q;
-    if (cum > U) {
-      if ((cum - U) < tol * sigma || (U - prev) < tol * sigma) *amb |= 1;
-      return (int32_t)s->idx[q];
-    }
-  }
-  *amb |= 1; /* u >= 1 or rounding: fall back to the last element with mass */
-  return last_pos >= 0 ? (int32_t)s->idx[last_pos] : (int32_t)s->idx[0];
+  int32_t id = walk_prefix(s, nP, u, tol, amb, 1);
+  if (alt) *alt = id;
+  if (alt && (*amb & 2) && nP_alt != nP) *alt = walk_prefix(s, nP_alt, u, tol, amb, 4);
+  return id;
 }
 
 void orc_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld,
                 const float* temps, const int32_t* top_k, const float* top_p,
                 const float* uniforms, int32_t* out_ids, uint8_t* out_amb, double tol,
-                int nthreads) {
+                int nthreads, int32_t* out_alt) {
   const char* base = (const char*)logits;
   size_t es = elem_size(dtype);
 #ifdef _OPENMP
@@ -302,14 +327,16 @@ void orc_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld,
     for (int64_t r = 0; r < B; ++r) {
       const void* row = base + (size_t)r * ld * es;
       uint8_t a = 0;
+      int32_t alt = 0;
       if (!temps) {
-        out_ids[r] = argmax_row(row, dtype, V);
+        out_ids[r] = alt = argmax_row(row, dtype, V);
       } else {
         out_ids[r] = sample_row(row, dtype, V, temps[r], top_k ? top_k[r] : 0,
                                 top_p ? top_p[r] : 1.0f, uniforms ? uniforms[r] : 0.0f, tol,
-                                &a, &s);
+                                &a, &alt, &s);
       }
       if (out_amb) out_amb[r] = a;
+      if (out_alt) out_alt[r] = alt;
     }
     free(s.keys);
     free(s.idx);

@@ -35,11 +35,16 @@ def test_mixed_depth_decode_step(lsg, orc, dev):
     rows = exit_idx
     x = wl["logits"][torch.from_numpy(rows).to(dev).long()].cpu().numpy()
     sel = lambda t: t.cpu().numpy()[rows]
-    want, amb = orc.sample(x, sel(wl["temperatures"]), sel(wl["top_k"]), sel(wl["top_p"]),
-                           sel(wl["uniforms"]))
+    want, amb, alt = orc.sample(x, sel(wl["temperatures"]), sel(wl["top_k"]), sel(wl["top_p"]),
+                                sel(wl["uniforms"]), with_alt=True)
     got = res.token_ids[:n].cpu().numpy()
-    bad = (got != want) & (amb == 0)
+    # the oracle's id, the other kept set's draw on a top-p-ambiguous row, or
+    # any id where the draw's CDF lies within 1e-6 of u
+    excused = ((amb & 1) != 0) | (((amb & 2) != 0) & ((amb & 4) != 0))
+    bad = (got != want) & ~(((amb & 2) != 0) & (got == alt)) & ~excused
     assert not bad.any(), np.nonzero(bad)
+    print(f"[parity] exited rows {n}: top-p-ambiguous {int(((amb & 2) != 0).sum())}, excused {int(excused.sum())}")
+    assert excused.sum() <= 3
 
 
 def test_gate_then_greedy(lsg, dev):

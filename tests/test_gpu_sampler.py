@@ -1,7 +1,9 @@
 """Parity of the HIP sampler (lsg_sample) with the CPU oracle and torch.argmax.
 
-Bar: greedy ids bit-exact; sampled ids equal except on rows the oracle flags as
-ambiguous (CDF within 1e-6 of the uniform, or top-p mass within 1e-6 of p).
+Bar: greedy ids bit-exact; sampled ids equal to the oracle's, except that a row
+whose top-p mass lies within 1e-6 of p may return the draw from the other kept
+set (the oracle computes it), and a row whose CDF lies within 1e-6 of the
+uniform (for the id drawn) is excused.  Each check caps the excused rows.
 """
 from __future__ import annotations
 
@@ -28,13 +30,24 @@ def _np(t):
     return None if t is None else t.detach().cpu().numpy()
 
 
-def check_sampling(lsg, orc, logits, T, K, P, U, max_amb_frac=0.01):
+def check_sampling(lsg, orc, logits, T, K, P, U, max_excused=0):
+    """The GPU ids against the oracle's on the same inputs.  Accepted per row:
+    the oracle's id; on a top-p-ambiguous row (amb bit 1) the draw from the
+    other kept set; excused (any id): a row whose draw's CDF lies within 1e-6 of
+    u (bit 0, or bit 2 when the GPU took the other kept set).  At most
+    max_excused rows may be excused."""
     ids = lsg.sample_rows(logits, T, K, P, U).cpu().numpy()
     arr, code = _host(orc, logits)
-    ref, amb = orc.sample(arr, _np(T), _np(K), _np(P), _np(U), dtype=code)
-    bad = np.nonzero((ids != ref) & (amb == 0))[0]
+    ref, amb, alt = orc.sample(arr, _np(T), _np(K), _np(P), _np(U), dtype=code, with_alt=True)
+    took_alt = ((amb & 2) != 0) & (ids == alt) & (ids != ref)
+    excused = ((amb & 1) != 0) | (((amb & 2) != 0) & ((amb & 4) != 0))
+    ok = (ids == ref) | took_alt | excused
+    bad = np.nonzero(~ok)[0]
     assert bad.size == 0, f"{bad.size} mismatching rows, e.g. row {bad[:5]}: gpu {ids[bad[:5]]} oracle {ref[bad[:5]]}"
-    assert (amb != 0).mean() <= max_amb_frac, f"too many ambiguous rows: {(amb != 0).sum()}"
+    print(f"[parity] rows {len(ids)}: top-p-ambiguous {int(((amb & 2) != 0).sum())} "
+          f"(other kept set taken {int(took_alt.sum())}), excused {int(excused.sum())} "
+          f"(differing {int((excused & (ids != ref)).sum())})")
+    assert excused.sum() <= max_excused, f"too many excused rows: {int(excused.sum())} > {max_excused}"
     assert ((ids >= 0) & (ids < logits.shape[1])).all()
     return ids, ref, amb
 
@@ -96,7 +109,7 @@ def test_sample_ouro_mixed(lsg, orc, dev):
     # near-flat logits: each token carries ~1/40000 of the mass, so a few top-p
     # boundaries fall within the 1e-6 ambiguity band
     check_sampling(lsg, orc, wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"], wl["uniforms"],
-                   max_amb_frac=0.05)
+                   max_excused=5)
 
 
 def test_sample_huginn_full(lsg, orc, dev):
@@ -110,7 +123,7 @@ def test_sample_mixed_depth_fp32(lsg, orc, dev):
     (T=1e-6)/top-k/top-p rows."""
     wl = lsg.workloads.cdb_mixed_depth(dev)
     ids, ref, amb = check_sampling(lsg, orc, wl["logits"], wl["temperatures"], wl["top_k"], wl["top_p"],
-                                   wl["uniforms"], max_amb_frac=0.05)
+                                   wl["uniforms"], max_excused=2)
     # greedy rows with tied maxima split their mass: the uniform decides the tie
     tie = wl["tie_rows"].cpu().numpy() & (wl["temperatures"].cpu().numpy() < 1e-5)
     if tie.any():
@@ -134,7 +147,7 @@ def test_modes_ragged(lsg, orc, dev, dtype, V):
     P = torch.tensor([1.0, 0.9, 0.5, 1.0, 0.99, 0.3, 0.95, 1.0] * 3, device=dev)
     U = torch.rand(B, generator=g, device=dev)
     for k_, p_ in ((K, P), (None, None), (K, None), (None, P)):
-        check_sampling(lsg, orc, x, T, k_, p_, U, max_amb_frac=0.35)
+        check_sampling(lsg, orc, x, T, k_, p_, U, max_excused=2)
 
 
 def test_flat_rows_exact_path(lsg, orc, dev):
@@ -146,7 +159,7 @@ def test_flat_rows_exact_path(lsg, orc, dev):
     P = torch.linspace(0.1, 0.99, B, device=dev)
     K = torch.tensor([-1] * 8 + [30000] * 8, dtype=torch.int32, device=dev)
     U = torch.rand(B, generator=g, device=dev)
-    check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.2)
+    check_sampling(lsg, orc, x, T, K, P, U, max_excused=1)
 
 
 def test_closed_forms_gpu(lsg, dev):
@@ -269,6 +282,37 @@ def test_sampler_prepare_and_sample(lsg, orc, dev, SP):
     assert ((a >= 0) & (a < 3000)).all()
 
 
+def test_filter_merge_batches_on_device(lsg, orc, dev, SP):
+    """A batch filtered to some of its rows and merged with another
+    (BatchSamplingArgs.filter_batch / merge_batch, sample.py:20-53), then sampled
+    on the device: ids against the oracle on the merged arguments, and the merged
+    rows carry their own arguments or the neutral defaults (T=1e-6, k=V, p=1)."""
+    from types import SimpleNamespace
+
+    V = 5000
+    s = lsg.Sampler(dev, V)
+    mk = lambda ps: s.prepare(SimpleNamespace(reqs=[SimpleNamespace(sampling_params=p) for p in ps]))
+    a = mk([SP(temperature=0.7, top_k=30), SP(), SP(temperature=1.1, top_p=0.85), SP(temperature=0.5),
+            SP(temperature=0.9, top_k=5, top_p=0.9), SP(top_k=1, temperature=1.0)])
+    b = mk([SP(temperature=0.8, top_p=0.9), SP(temperature=1.3, top_p=0.7), SP(temperature=0.6, top_p=0.95),
+            SP(temperature=1.0, top_p=0.8)])
+    g = torch.Generator(device=dev).manual_seed(41)
+    a.uniforms = torch.rand(6, device=dev, generator=g)
+    b.uniforms = torch.rand(4, device=dev, generator=g)
+    keep = torch.tensor([4, 0, 2], device=dev)
+    af = a.filter_batch(keep, False, need_top_k=True, need_top_p=True)
+    assert b.top_k is None  # the second batch has no top-k rows: merge fills k = V
+    m = af.merge_batch(b, 3, 4, V)
+    assert torch.equal(m.temperatures[:3], a.temperatures[keep]) and torch.equal(m.temperatures[3:], b.temperatures)
+    assert torch.equal(m.top_k[:3], a.top_k[keep]) and (m.top_k[3:] == V).all()
+    assert torch.equal(m.top_p[:3], a.top_p[keep]) and torch.equal(m.top_p[3:], b.top_p)
+    assert torch.equal(m.uniforms, torch.cat([a.uniforms[keep], b.uniforms]))
+    x = torch.randn(7, V, device=dev, generator=g)
+    ids = s.sample(x, m)
+    got, _, _ = check_sampling(lsg, orc, x, m.temperatures, m.top_k, m.top_p, m.uniforms)
+    assert torch.equal(ids.cpu(), torch.from_numpy(got))
+
+
 # ------------------------------------------- large batches (B > 2 x CUs) ----
 def _mixed_params(B, V, g, dev):
     """Per-row modes cycling through greedy-in-batch (T=1e-6), no filter,
@@ -294,8 +338,8 @@ def test_large_batches(lsg, orc, dev, dtype, V):
     x[9, :] = float("-inf")
     x[9, V - 1] = 2.0
     T, K, P, U = _mixed_params(B, V, g, dev)
-    check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.05)
-    check_sampling(lsg, orc, x, T, None, None, U, max_amb_frac=0.05)
+    check_sampling(lsg, orc, x, T, K, P, U, max_excused=20)
+    check_sampling(lsg, orc, x, T, None, None, U, max_excused=20)
     ids = lsg.sample_rows(x, None, None, None, None)
     assert torch.equal(ids.long(), torch.argmax(x, -1))
 
@@ -326,7 +370,7 @@ def test_streamed_rows_edge_cases(lsg, orc, dev, dtype, V):
     ids = lsg.sample_rows(x, None, None, None, None).cpu().numpy()
     assert np.array_equal(ids, torch.argmax(x, dim=-1).to(torch.int32).cpu().numpy())
     T, K, P, U = _mixed_params(B, V, g, dev)
-    ids, _, _ = check_sampling(lsg, orc, x, T, K, P, U, max_amb_frac=0.05)
+    ids, _, _ = check_sampling(lsg, orc, x, T, K, P, U, max_excused=8)
     assert ids[8] % 5 != 0 and ids[10] == 12345
 
 

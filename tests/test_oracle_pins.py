@@ -172,6 +172,24 @@ def test_ambiguity_flag_is_tight(orc):
     assert ids[1] == 2
 
 
+def test_topp_alternative_draw(orc):
+    """Rows whose top-p mass sits on p: the oracle also gives the draw from the
+    other kept set.  Masses 1 : 1/2 : 1/2 (x = ln 2, 0, 0 at T = 1), u = 0.9:
+    p = 1/2 puts the first element's mass on the target (kept set {0}, id 0;
+    alternative {0, 1, 2}, U = 1.8 of 2 -> id 2); p just above 1/2 puts the
+    tied pair's lower edge on it (kept set {0, 1, 2}, id 2; alternative {0})."""
+    x = np.array([[np.log(2.0), 0.0, 0.0]] * 2, np.float32)
+    p = np.array([0.5, 0.5 + 1e-8], np.float32)
+    p[1] = np.nextafter(np.float32(0.5), np.float32(1.0))
+    ids, amb, alt = orc.sample(x, np.ones(2, np.float32), None, p, np.full(2, 0.9, np.float32), with_alt=True)
+    assert amb[0] & 2 and ids[0] == 0 and alt[0] == 2
+    assert amb[1] & 2 and ids[1] == 2 and alt[1] == 0
+    # far from the boundary: no flag, the alternative is the draw itself
+    ids, amb, alt = orc.sample(x, np.ones(2, np.float32), None, np.array([0.3, 0.8], np.float32),
+                               np.full(2, 0.9, np.float32), with_alt=True)
+    assert (amb == 0).all() and (alt == ids).all() and ids.tolist() == [0, 2]
+
+
 # ------------------------------------------------------------ exit gate -----
 def _logit(p):
     return float(np.log(p / (1 - p)))
