@@ -51,7 +51,7 @@ def _parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="sample_huginn",
-                    choices=["sample_huginn", "sample_ouro", "gate_cdb", "cdb_mixed_depth"])
+                    choices=["sample_huginn", "sample_ouro", "gate_cdb", "cdb_mixed_depth", "coda_ouro"])
     ap.add_argument("--nbuf", type=int, default=0, help="logits buffers rotated (0: auto, > 512 MB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=0, help="rows in the CPU baseline sample (0: auto)")
@@ -359,6 +359,77 @@ def main():
                 "frac": alg / per_launch / 1e9 / HBM_PEAK_GBS,
                 "traffic": _traffic_from_profiles(a.workload),
             },
+            "cpu_baseline": cpu,
+        }
+    elif a.workload == "coda_ouro":  # the fused coda tail: LM-head projection + token step
+        B, H, V = 256, 2048, 49152
+        g = torch.Generator(device=dev).manual_seed(1)
+        h = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
+        nW = 3  # 3 x 201 MB of weights rotate, beyond the 256 MB Infinity Cache
+        Ws = [(torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(nW)]
+        T = 0.3 + 0.9 * torch.rand(B, generator=g, device=dev)
+        Kt = torch.tensor([1, 20, 50, V], dtype=torch.int32, device=dev)[
+            torch.randint(0, 4, (B,), generator=g, device=dev)].contiguous()
+        P = 0.8 + 0.2 * torch.rand(B, generator=g, device=dev)
+        U = torch.rand(B, generator=g, device=dev)
+        args = pkg.BatchSamplingArgs(T, Kt, P, U)
+        ws = torch.empty(pkg.coda.workspace_bytes(B, V), dtype=torch.uint8, device=dev)
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        lg = torch.empty(B, V, dtype=torch.bfloat16, device=dev)
+
+        def launch(i):
+            pkg.coda.coda_sample(h, Ws[i % nW], args, workspace=ws, out=ids)
+
+        def launch_gemm(i):
+            pkg.coda.lm_head(h, Ws[i % nW], out=lg)
+
+        if a.traffic_probe:
+            _probe(torch, launch_gemm, dev)
+            return
+        times = _time_graph(torch, launch, K, W)
+        secs = _median(times)
+        per = secs / K
+        gtimes = _time_graph(torch, launch_gemm, K, W)
+        gper = _median(gtimes) / K
+        ntiles = -(-V // 192)
+        gemm_bytes = V * H * 2 + B * H * 2 + B * V * 2 + B * ntiles * 8  # W, h, bf16 logits, tile maxima
+        flops = 2.0 * B * H * V
+        cpu = None
+        if not a.no_cpu_baseline:
+            rows = a.cpu_rows or 16
+            hc, Wc = h[:rows].cpu(), Ws[0].cpu()
+            sel = lambda t: t[:rows].cpu()
+            Tc, Kc, Pc, Uc = sel(T), sel(Kt), sel(P), sel(U)
+            prev = torch.get_num_threads()
+            r = {}
+            try:
+                for n in (_host_threads(), 1):
+                    torch.set_num_threads(n)
+                    step = lambda: _torch_cpu_sampling(
+                        torch, torch.nn.functional.linear(hc, Wc).float(), Tc, Kc, Pc, Uc)
+                    r[n] = rows * _timed_threads(torch, step, 5.0 if n > 1 else 10.0)
+            finally:
+                torch.set_num_threads(prev)
+            (na, va), (_, v1) = list(r.items())[0], list(r.items())[-1]
+            cpu = {"value": va, "unit": "rows/s", "cores": na, "kind": "port", "value_1_core": v1,
+                   "cores_1_core": 1,
+                   "sample": f"first {rows} rows: torch on the CPU, F.linear in bf16 against the full "
+                             f"[{V}, {H}] weight, then the sampling restatement; repeated for 5 s (10 s at 1 thread)"}
+        result = {
+            "metric": "coda rows/sec (LM-head projection + token step), B=256 H=2048 V=49152 bf16",
+            "value": B / per, "unit": "rows/s", "n_gpus": 1, "steps": K, "warmup": W,
+            "ms_per_step": per * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "coda_ouro: h [256, 2048] bf16 N(0,1), W [49152, 2048] bf16 N(0, 0.02^2), "
+                                   "mixed T/top_k/top_p", "batch": B, "hidden": H, "vocab": V,
+                       "rotated_weights": nW},
+            "timing": _timing(times, K),
+            "projection": {"ms_per_launch": gper * 1e3, "timing": _timing(gtimes, K),
+                           "mfma_tflops": flops / gper / 1e12, "mfma_peak_tflops": 2500.0,
+                           "mfma_frac": flops / gper / 1e12 / 2500.0},
+            "roofline": {"bound": "hbm", "achieved": gemm_bytes / gper / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gemm_bytes / gper / 1e9 / HBM_PEAK_GBS,
+                         "traffic": _traffic_from_profiles(a.workload)},
             "cpu_baseline": cpu,
         }
     else:  # gate_cdb: the 4-step exit gate with compaction (latency-bound)

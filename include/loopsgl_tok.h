@@ -182,6 +182,38 @@ int lsg_relative_state_change(const void* h, const void* h_prev, int dtype, int6
 /* Workspace bytes needed by an op (LSG_OP_*) for B rows. */
 size_t lsg_workspace_bytes(int op, int64_t B);
 
+/*
+ * The coda's vocabulary projection (ParallelLMHead.forward,
+ * python/loopsgl/layers/embedding.py:88-111, tp_size 1; called from
+ * BaseLoopedForCausalLM.forward_coda, models/looped/base.py:166-168):
+ *   logits[b, v] = bf16(sum_k hidden[b, k] * weight[v, k])
+ * on MFMA with fp32 accumulation (the reference's F.linear in bf16).
+ *   hidden  bf16 [B, H], row stride ld_hidden;  weight  bf16 [V, H], row stride
+ *           ld_weight; H a multiple of 64, strides multiples of 8 (>= H), both
+ *           16-byte aligned.
+ *   logits  bf16 [B, V] out, row stride ld_logits >= V.
+ */
+int lsg_lm_head(const void* hidden, int64_t B, int64_t H, int64_t ld_hidden, const void* weight, int64_t V,
+                int64_t ld_weight, void* logits, int64_t ld_logits, void* stream);
+
+/*
+ * The fused coda tail: the projection above followed by the token step, with
+ * no fp32 [B, V] logits buffer.  Replaces lm_head -> the copy into
+ * GraphCaptureBuffer.logits (model_executor/graph.py:34,
+ * model_executor/cdb_graph.py:80-82) -> Sampler.sample (sample.py:107-112).
+ * The bf16 logits and, per row and 192-column tile, their maximum and first
+ * index go to the workspace; temperatures == NULL (all greedy) finishes from
+ * the tile maxima alone (torch.argmax rules), otherwise lsg_sample runs on the
+ * bf16 logits with the same per-row arguments as lsg_sample.
+ *   workspace  >= lsg_lm_head_workspace_bytes(B, V) bytes, 16-byte aligned
+ *              (contents need no initialisation).
+ */
+int lsg_lm_head_sample(const void* hidden, int64_t B, int64_t H, int64_t ld_hidden, const void* weight, int64_t V,
+                       int64_t ld_weight, const float* temperatures, const int32_t* top_k, const float* top_p,
+                       const float* uniforms, void* workspace, size_t workspace_bytes, int32_t* out_ids,
+                       void* stream);
+size_t lsg_lm_head_workspace_bytes(int64_t B, int64_t V);
+
 /* Message of the last failed call on this host thread ("" if none). */
 const char* lsg_last_error(void);
 

@@ -11,6 +11,8 @@ kernels in ``libloopsgl_tok.so`` (C ABI: include/loopsgl_tok.h):
   integration  exit_signal / sample bindings for the reference's own model
                and sampler objects
   decode_step  gate -> on-device exit compaction -> sampling of exited rows
+  coda         lm_head / coda_sample: the vocabulary projection (MFMA) and the
+               token step without an fp32 logits buffer (layers/embedding.py)
 
 The directory name contains a hyphen, so import it through
 ``__graft_entry__.package()`` (registers it as ``loop_sglang_amd``).
@@ -26,10 +28,10 @@ from .exit_gate import (
     relative_state_change,
 )
 from .sampler import BatchSamplingArgs, Sampler, make_device_tensor, sample_impl, sample_rows
-from . import integration, workloads
+from . import coda, integration, workloads
 
 __all__ = [
-    "BatchSamplingArgs", "DecodeStepResult", "GateResult", "HuginnExitGate", "OuroExitGate",
+    "BatchSamplingArgs", "coda", "DecodeStepResult", "GateResult", "HuginnExitGate", "OuroExitGate",
     "RouteResult", "Sampler", "cdb_decode_step", "cumulative_exit_probability", "integration", "ouro_exit_signal",
     "make_device_tensor", "relative_state_change", "sample_impl", "sample_rows",
 ]

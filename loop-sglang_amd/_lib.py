@@ -33,6 +33,9 @@ SIGNATURES = {
     "lsg_cumulative_exit_probability": (ctypes.c_int, [_P, ctypes.c_int, _P, _P, _I64, _P]),
     "lsg_relative_state_change": (ctypes.c_int, [_P, _P, ctypes.c_int, _I64, _I64, _I64, _I64, _F, _F, _P,
                                                  _P, _P, _P, _P, _P, _SZ, _P]),
+    "lsg_lm_head": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "lsg_lm_head_sample": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _SZ, _P, _P]),
+    "lsg_lm_head_workspace_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "lsg_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _I64]),
     "lsg_last_error": (ctypes.c_char_p, []),
     "lsg_version": (ctypes.c_int, []),

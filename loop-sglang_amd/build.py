@@ -34,6 +34,7 @@ SOURCES = {
     "sample.hip": ["-ffp-contract=fast"],
     "sample_quad.hip": ["-ffp-contract=fast"],
     "exit_gate.hip": ["-ffp-contract=off"],
+    "lm_head.hip": [],
     "capi.hip": [],
 }
 
