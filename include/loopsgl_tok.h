@@ -201,7 +201,7 @@ int lsg_lm_head(const void* hidden, int64_t B, int64_t H, int64_t ld_hidden, con
  * no fp32 [B, V] logits buffer.  Replaces lm_head -> the copy into
  * GraphCaptureBuffer.logits (model_executor/graph.py:34,
  * model_executor/cdb_graph.py:80-82) -> Sampler.sample (sample.py:107-112).
- * The bf16 logits and, per row and 192-column tile, their maximum and first
+ * The bf16 logits and, per row and 96-column tile, their maximum and first
  * index go to the workspace; temperatures == NULL (all greedy) finishes from
  * the tile maxima alone (torch.argmax rules), otherwise lsg_sample runs on the
  * bf16 logits with the same per-row arguments as lsg_sample.

@@ -11,23 +11,27 @@
 // the sampler re-reads that (12 bytes of logits traffic per vocabulary entry);
 // here the projection writes the bf16 logits once (the values the reference's
 // F.linear returns, up to the accumulation order of fp32 sums) with, per row
-// and 192-column tile, the maximum and its first index, so greedy rows finish
+// and 96-column tile, the maximum and its first index, so greedy rows finish
 // from those alone and sampled rows read the bf16 logits once.
 //
 // lm_head_kernel: C[b, v] = bf16(sum_k h[b, k] * W[v, k]) on MFMA
 // (v_mfma_f32_32x32x16_bf16, fp32 accumulation).  One 256-thread workgroup per
 // (256-row batch tile, 192-column vocabulary tile); W is streamed from HBM once
-// per batch tile, h is re-read from L2.  K advances in steps of 64 through two
-// LDS stages (rows padded to 144 bytes so the fragment reads are free of bank
-// conflicts): the next stage's global loads are issued before the current
-// stage's MFMAs.  Wave w owns batch rows 64w .. 64w+63 of the tile and all 192
-// columns: 2 x 6 blocks of 32 x 32, 192 fp32 accumulators per lane.
+// per batch tile, h is re-read from L2.  K advances in steps of 32 through five
+// LDS stages filled by direct-to-LDS loads (no register staging), four stages
+// ahead of the MFMAs, so ~112 KB per compute unit are in flight to cover the
+// memory latency.  A stage row is 64 bytes (four 16-byte chunks), chunk c of
+// row r stored at position c ^ (((r >> 1) ^ (r >> 2)) & 3), so the 16-byte
+// fragment reads of eight (or sixteen) consecutive rows hit distinct banks.  Eight waves (two per SIMD):
+// wave w owns batch rows 64 (w % 4) .. +63 of the tile and columns
+// 96 (w / 4) .. +95: 2 x 3 blocks of 32 x 32, 96 fp32 accumulators per lane.
 // Operand layouts (checked on the device): A lane l holds row l % 32,
 // k = 8 (l / 32) + q; B lane l holds column l % 32, same k; C lane l, register
 // r holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 // Epilogue: the accumulators are rounded to bf16 (RNE) into LDS, then stored
-// as 16-byte rows segments; lane l of wave w then scans row 64w + l of the tile
-// for its maximum and first index (torch.argmax rules: NaN wins, first wins).
+// as 16-byte row segments; lane l of wave w then scans its 96 columns of row
+// 64 (w % 4) + l for their maximum and first index (torch.argmax rules: NaN
+// wins, first wins): row statistics per 96-column half tile.
 //
 // lm_head_argmax_kernel: per row, the first maximum over the tiles' maxima.
 #include <hip/hip_runtime.h>
@@ -41,14 +45,21 @@ namespace lmh {
 
 constexpr int kMT = 256;   // batch rows per tile
 constexpr int kNT = 192;   // vocabulary columns per tile
-constexpr int kKT = 64;    // K per stage
-constexpr int kRow = 72;   // LDS row stride in bf16 (64 + 8 padding: 144 bytes)
-constexpr int kThreads = 256;
+constexpr int kKT = 32;    // K per stage
+constexpr int kRow = 32;   // LDS row stride in bf16 (64 bytes, swizzled)
+constexpr int kStages = 5;  // LDS stages (four in flight ahead of the MFMAs)
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int kHalf = kNT / 2;  // columns per wave, and per row-statistics tile
 constexpr int kStageA = kMT * kRow;  // bf16 elements of h per stage
 constexpr int kStageB = kNT * kRow;  // bf16 elements of W per stage
-constexpr int kLdsElems = 2 * (kStageA + kStageB);
-// epilogue: 64 rows x 192 columns of bf16 per wave, rows padded by 8
-constexpr int kOutRow = kNT + 8;
+constexpr int kLdsElems = kStages * (kStageA + kStageB);
+// direct-to-LDS loads per wave per stage, 1 KB (16 rows) each: h's 16 row
+// groups two per wave; W's 12 groups two per wave (waves 4-7 load their own
+// group twice, the same bytes to the same place)
+constexpr int kLoadsA = 2, kLoadsB = 2, kLoads = kLoadsA + kLoadsB;
+// epilogue: 64 rows x 96 columns of bf16 per wave, rows padded by 8
+constexpr int kOutRow = kHalf + 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -58,7 +69,7 @@ struct Params {
   const uint16_t* h;   // [B, H] bf16, row stride ldh
   const uint16_t* w;   // [V, H] bf16, row stride ldw
   uint16_t* logits;    // [B, V] bf16, row stride ldl
-  float* tmax;         // [B, ntiles] tile maxima (may be null)
+  float* tmax;         // [B, ntiles] maxima per 96-column half tile (may be null)
   int32_t* targ;       // [B, ntiles] their first indices
   int64_t B, H, V, ldh, ldw, ldl;
   int ntiles;
@@ -71,44 +82,43 @@ __device__ __forceinline__ uint16_t f2bf(float f) {  // round to nearest even; N
 }
 __device__ __forceinline__ float bf2f(uint32_t u16) { return __uint_as_float(u16 << 16); }
 
-// Global -> registers for one stage: thread t holds h chunks t + 256 i (i < 8)
-// and W chunks t + 256 i (i < 6) of 16 bytes; chunk c is row c / 8, 16-byte
-// column c % 8 of the stage.  Rows outside the matrices read as zero.
-struct StageRegs {
-  v4u a[8];
-  v4u b[6];
-};
+// Stage s of K into LDS buffer s % kStages by direct-to-LDS loads: a load of
+// row group g writes rows 16 g .. 16 g + 15 of the stage (1 KB, lane i at byte
+// 16 i: row i / 4, position i % 4), reading the chunk that belongs at that
+// position.  Rows outside the matrices read the last row (their results are
+// never stored).
+__device__ __forceinline__ int swz(int row, int c) { return c ^ (((row >> 1) ^ (row >> 2)) & 3); }
 
-__device__ __forceinline__ void load_stage(const Params& P, int64_t m0, int64_t n0, int64_t k0, StageRegs& r) {
-  const int t = threadIdx.x;
+__device__ __forceinline__ void issue_stage(const Params& P, uint16_t* lds, int64_t m0, int64_t n0, int s, int kb) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  uint16_t* A = lds + (s % kStages) * (kStageA + kStageB);
+  uint16_t* Bm = A + kStageA;
+  const int64_t k0 = (int64_t)kb * kKT;
+  const int rl = lane >> 2, pos = lane & 3;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = t + kThreads * i, row = c >> 3, cc = c & 7;
-    const int64_t gr = m0 + row;
-    r.a[i] = gr < P.B ? *reinterpret_cast<const v4u*>(P.h + gr * P.ldh + k0 + cc * 8) : v4u{0u, 0u, 0u, 0u};
+  for (int q = 0; q < kLoadsA; ++q) {
+    const int g = q * kWaves + wid;
+    const int row = 16 * g + rl;
+    int64_t gr = m0 + row;
+    gr = gr < P.B ? gr : P.B - 1;
+    const uint16_t* src = P.h + gr * P.ldh + k0 + swz(row, pos) * 8;
+    __builtin_amdgcn_global_load_lds(src, A + 16 * g * kRow, 16, 0, 0);
   }
 #pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const int c = t + kThreads * i, row = c >> 3, cc = c & 7;
-    const int64_t gr = n0 + row;
-    r.b[i] = gr < P.V ? *reinterpret_cast<const v4u*>(P.w + gr * P.ldw + k0 + cc * 8) : v4u{0u, 0u, 0u, 0u};
+  for (int q = 0; q < kLoadsB; ++q) {
+    const int g = q == 0 ? wid : (wid < 4 ? wid + kWaves : wid);
+    const int row = 16 * g + rl;
+    int64_t gr = n0 + row;
+    gr = gr < P.V ? gr : P.V - 1;
+    const uint16_t* src = P.w + gr * P.ldw + k0 + swz(row, pos) * 8;
+    __builtin_amdgcn_global_load_lds(src, Bm + 16 * g * kRow, 16, 0, 0);
   }
 }
 
-__device__ __forceinline__ void store_stage(uint16_t* lds, int stage, const StageRegs& r) {
-  uint16_t* A = lds + stage * (kStageA + kStageB);
-  uint16_t* Bm = A + kStageA;
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = t + kThreads * i, row = c >> 3, cc = c & 7;
-    *reinterpret_cast<v4u*>(A + row * kRow + cc * 8) = r.a[i];
-  }
-#pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const int c = t + kThreads * i, row = c >> 3, cc = c & 7;
-    *reinterpret_cast<v4u*>(Bm + row * kRow + cc * 8) = r.b[i];
-  }
+// Wait until at most n of this wave's loads are outstanding (n < 64).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) void lm_head_kernel(Params P) {
@@ -116,44 +126,59 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) v
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t n0 = (int64_t)blockIdx.x * kNT, m0 = (int64_t)blockIdx.y * kMT;
   const int nst = (int)(P.H / kKT);
-  f32x16 acc[2][6];
+  const int wr = (wid & 3) * 64, wc = (wid >> 2) * kHalf;  // this wave's rows and columns of the tile
+  f32x16 acc[2][3];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 6; ++j) acc[i][j] = f32x16{};
-  StageRegs r;
-  load_stage(P, m0, n0, 0, r);
-  store_stage(lds, 0, r);
-  __syncthreads();
-  const int fr = lane & 31, fk = (lane >> 5) * 8;  // fragment row/column and k offset of this lane
+    for (int j = 0; j < 3; ++j) acc[i][j] = f32x16{};
+  const int fr = lane & 31, fk = lane >> 5;  // fragment row/column and k chunk of this lane
+  // Each workgroup starts at its own K block (and wraps around), so that at any
+  // moment the workgroups read different 64-byte columns of their W rows: rows
+  // 2^k bytes apart read at one offset would all land on the same HBM channel.
+  const int kshift = (int)(blockIdx.x % (unsigned)nst);
+  auto kblock = [&](int s) { const int b = s + kshift; return b >= nst ? b - nst : b; };
+#pragma unroll
+  for (int q = 0; q < kStages - 1; ++q)
+    if (q < nst) issue_stage(P, lds, m0, n0, q, kblock(q));
   for (int s = 0; s < nst; ++s) {
-    const bool more = s + 1 < nst;
-    if (more) load_stage(P, m0, n0, (int64_t)(s + 1) * kKT, r);
-    const uint16_t* A = lds + (s & 1) * (kStageA + kStageB);
+    // stage s complete for this wave (loads retire in order), then for all
+    const int ahead = nst - 1 - s;
+    if (ahead >= 3) wait_vm<3 * kLoads>();
+    else if (ahead == 2) wait_vm<2 * kLoads>();
+    else if (ahead == 1) wait_vm<kLoads>();
+    else wait_vm<0>();
+    __syncthreads();  // also: every wave is done with stage s - 1's buffer
+    if (s + kStages - 1 < nst) issue_stage(P, lds, m0, n0, s + kStages - 1, kblock(s + kStages - 1));
+    const uint16_t* A = lds + (s % kStages) * (kStageA + kStageB);
     const uint16_t* Bm = A + kStageA;
 #pragma unroll
-    for (int kk = 0; kk < kKT; kk += 16) {
-      bf16x8 af[2], bfr[6];
+    for (int kk = 0; kk < kKT / 16; ++kk) {
+      const int c = 2 * kk + fk;  // 16-byte chunk of k
+      bf16x8 af[2], bfr[3];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wr + i * 32 + fr;
+        af[i] = *reinterpret_cast<const bf16x8*>(A + row * kRow + swz(row, c) * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int row = wc + j * 32 + fr;
+        bfr[j] = *reinterpret_cast<const bf16x8*>(Bm + row * kRow + swz(row, c) * 8);
+      }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(A + (wid * 64 + i * 32 + fr) * kRow + kk + fk);
 #pragma unroll
-      for (int j = 0; j < 6; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(Bm + (j * 32 + fr) * kRow + kk + fk);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 6; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 3; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_stage(lds, (s + 1) & 1, r);
-    __syncthreads();
   }
-  // epilogue: bf16 tile of this wave (64 rows x 192 columns) through LDS
+  __syncthreads();  // every wave is done with the stages before the epilogue reuses LDS
+  // epilogue: bf16 tile of this wave (64 rows x 96 columns) through LDS
   uint16_t* O = lds + wid * 64 * kOutRow;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 6; ++j)
+    for (int j = 0; j < 3; ++j)
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int row = i * 32 + (q >> 2) * 8 + (lane >> 5) * 4 + (q & 3);
@@ -161,14 +186,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) v
       }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
-  // 16-byte stores: row segments of 24 chunks, lane l takes chunks l, l + 64, ...
-  const int64_t nvalid = P.V - n0 < kNT ? P.V - n0 : kNT;
-  const bool vec = (P.ldl % 8) == 0 && nvalid == kNT && (reinterpret_cast<uintptr_t>(P.logits) & 15u) == 0;
-  for (int c = lane; c < 64 * (kNT / 8); c += 64) {
-    const int row = c / (kNT / 8), cc = c % (kNT / 8);
-    const int64_t gr = m0 + wid * 64 + row;
-    if (gr >= P.B) continue;
-    uint16_t* dst = P.logits + gr * P.ldl + n0 + cc * 8;
+  // 16-byte stores: row segments of 12 chunks, lane l takes chunks l, l + 64, ...
+  const int64_t c0 = n0 + wc;  // first column of this wave
+  const int64_t nv = P.V - c0 < 0 ? 0 : (P.V - c0 < kHalf ? P.V - c0 : kHalf);
+  const bool vec = (P.ldl % 8) == 0 && nv == kHalf && (reinterpret_cast<uintptr_t>(P.logits) & 15u) == 0;
+  for (int c = lane; c < 64 * (kHalf / 8); c += 64) {
+    const int row = c / (kHalf / 8), cc = c % (kHalf / 8);
+    const int64_t gr = m0 + wr + row;
+    if (gr >= P.B || cc * 8 >= nv) continue;
+    uint16_t* dst = P.logits + gr * P.ldl + c0 + cc * 8;
     const v4u v = *reinterpret_cast<const v4u*>(O + row * kOutRow + cc * 8);
     if (vec) {
       *reinterpret_cast<v4u*>(dst) = v;
@@ -176,24 +202,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) v
       const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (cc * 8 + e < nvalid) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+        if (cc * 8 + e < nv) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
     }
   }
-  // tile maximum and its first index for row 64 wid + lane
+  // maximum and first index of this wave's 96 columns of row wr + lane
   if (P.tmax) {
-    const int64_t gr = m0 + wid * 64 + lane;
+    const int64_t gr = m0 + wr + lane;
     if (gr < P.B) {
       float mx = -INFINITY;
       int arg = -1;
       bool nan = false;
-      for (int cc = 0; cc < kNT / 8; ++cc) {
+      for (int cc = 0; cc < kHalf / 8; ++cc) {
         const v4u v = *reinterpret_cast<const v4u*>(O + lane * kOutRow + cc * 8);
         const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int c = cc * 8 + e;
           const float x = bf2f((w4[e >> 1] >> (16 * (e & 1))) & 0xffffu);
-          if (nan || c >= nvalid) continue;
+          if (nan || c >= nv) continue;
           if (x != x) {
             nan = true;
             mx = x;
@@ -204,8 +230,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) v
           }
         }
       }
-      P.tmax[gr * P.ntiles + blockIdx.x] = mx;
-      P.targ[gr * P.ntiles + blockIdx.x] = (int32_t)(n0 + arg);
+      const int64_t t = (int64_t)blockIdx.x * 2 + (wid >> 2);
+      P.tmax[gr * P.ntiles + t] = mx;
+      P.targ[gr * P.ntiles + t] = arg < 0 ? 0x7fffffff : (int32_t)(c0 + arg);  // an empty half: no entry
     }
   }
 }
@@ -224,7 +251,7 @@ __global__ __launch_bounds__(64) void lm_head_argmax_kernel(const float* tmax, c
   for (int t = lane; t < ntiles; t += 64) {
     const float x = tmax[b * ntiles + t];
     const int a = targ[b * ntiles + t];
-    if (nan) continue;
+    if (nan || a == 0x7fffffff) continue;  // an empty half tile
     if (x != x) {
       nan = true;
       arg = a;
@@ -248,11 +275,12 @@ __global__ __launch_bounds__(64) void lm_head_argmax_kernel(const float* tmax, c
 
 size_t lm_head_lds_bytes() {
   const size_t stages = (size_t)lmh::kLdsElems * 2;
-  const size_t out = (size_t)4 * 64 * lmh::kOutRow * 2;
+  const size_t out = (size_t)lmh::kWaves * 64 * lmh::kOutRow * 2;
   return stages > out ? stages : out;
 }
 
-int lm_head_tiles(int64_t V) { return (int)((V + lmh::kNT - 1) / lmh::kNT); }
+// Row-statistics tiles: two per 192-column projection tile.
+int lm_head_tiles(int64_t V) { return (int)(2 * ((V + lmh::kNT - 1) / lmh::kNT)); }
 
 int lm_head_launch(const void* h, int64_t B, int64_t H, int64_t ldh, const void* w, int64_t V, int64_t ldw,
                    void* logits, int64_t ldl, float* tmax, int32_t* targ, hipStream_t st) {
@@ -269,7 +297,7 @@ int lm_head_launch(const void* h, int64_t B, int64_t H, int64_t ldh, const void*
   P.ldw = ldw;
   P.ldl = ldl;
   P.ntiles = lm_head_tiles(V);
-  const dim3 grid((unsigned)P.ntiles, (unsigned)((B + lmh::kMT - 1) / lmh::kMT));
+  const dim3 grid((unsigned)((V + lmh::kNT - 1) / lmh::kNT), (unsigned)((B + lmh::kMT - 1) / lmh::kMT));
   static bool attr_set[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(LSG_ERR_HIP, "lm_head: no device");
