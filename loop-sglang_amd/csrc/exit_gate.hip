@@ -257,14 +257,23 @@ __global__ __launch_bounds__(kGateThreads) void ouro_gate_kernel(GateParams P) {
   const int64_t row = (int64_t)blockIdx.x * kGateRows + wid;
   const bool leader = lane == 0;
   const bool live = row < P.B;
-  // per-row scalars first, so their latency hides under the row loads
+  // per-row scalars first, so their latency hides under the row loads (the
+  // state of a row indexed through a state-pool slot waits for the slot)
   uint32_t serial = 0;
   if (P.serial) serial = __hip_atomic_load(P.serial, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int64_t s = row;
   int32_t ls = P.loop_step_scalar;
+  float bv = 0.0f, F = 0.0f;
+  long long pend = 0;
   if (live && leader) {
-    if (P.slots) s = P.slots[row];
+    if (P.bias) bv = load_one<T>(P.bias);
     if (P.loop_step) ls = P.loop_step[row];
+    if (P.slots) {
+      s = P.slots[row];
+    } else {
+      if (P.F_prev) F = P.F_prev[row];
+      if (!P.direct) pend = P.pending[row];
+    }
   }
   float acc = 0.0f;
   if (live) {
@@ -272,16 +281,13 @@ __global__ __launch_bounds__(kGateThreads) void ouro_gate_kernel(GateParams P) {
     row_pairs<T, kWave, VEC>(hrow, reinterpret_cast<const T*>(P.w), P.H, lane,
                              [&](float x, float y) { acc = fmaf(x, y, acc); });
   }
-  float F = 0.0f;
-  long long pend = 0;
-  if (live && leader) {
+  if (live && leader && P.slots) {
     if (P.F_prev) F = P.F_prev[s];
     if (!P.direct) pend = P.pending[s];
   }
   acc = wave_total(acc);
   int r = 0;
   if (live && leader) {
-    const float bv = P.bias ? load_one<T>(P.bias) : 0.0f;
     const float z = round_to<T>(acc + bv);
     const float Fn = gate_update(F, z);
     const int32_t depth = ls + 1;
