@@ -62,6 +62,7 @@ constexpr int kLoadWindow = 16;
 constexpr int kWavesPerEU = 4;
 constexpr int kHB = 128;          // coarse histogram: bins of 1/4 binary order over y in [-32, 0]
 constexpr int kFB = 256;          // fine histogram: bins of 1/8 binary order over y in [-32, 0]
+constexpr int kFarBin0 = 0x42000000 >> 18;  // float bits of 32.0 >> 18: far-floor bin 1 starts at d = 32
 constexpr int kWin = 512;         // window finished by one wave
 constexpr int kHPL = kWin / kWave;  // window entries per lane in the finish
 constexpr int kRB = 256;          // refinement bins per level
@@ -1271,6 +1272,7 @@ void quad_sample_kernel(SampleParams P) {
   float m = -INFINITY;
   if (tvalid) {
     if (kon || pon) S.wh[wid][lane] = S.wh[wid][lane + kWave] = 0u;  // this wave's histogram (a wave's LDS ops stay in order)
+    if (kon && threadIdx.x < kFB) S.fcnt[threadIdx.x] = 0u;   // the far-floor histogram (ordered by barrier 1)
     publish<T, CAP>(lane_pass<false>(R, c, S), c, kon, pon, S);
     stamp(1);
     __syncthreads();
@@ -1349,10 +1351,53 @@ void quad_sample_kernel(SampleParams P) {
     }
     bstar = lb < 0 ? -1 : 2 * lb + hb;
   }
-  stamp(3);
   float Lm = -INFINITY;
-  if (bstar >= 0) {
+  bool flr = bstar >= 0;
+  if (flr) {
     Lm = -0.25f * (float)(bstar + 1) - 0x1p-8f;
+  } else if (kon && k <= 2 * NW * kWave) {
+    // The k-th largest element lies more than 32 binary orders below the
+    // maximum (heavy tails, low temperature): bin the lanes' two largest pair
+    // maxima (distinct elements) by their distance d = -y below it, bin 0 for
+    // d <= 32, then 1/32 binary order per bin (the float bits of d from 32
+    // on; bin kFB - 1 collects the rest).  The top bins holding k of them
+    // bound the k-th largest element from below.
+    const v4u lt = S.lt[threadIdx.x];
+    auto far_bin = [&](uint32_t xb) {
+      const float y = (__uint_as_float(xb) - m) * c;
+      return y >= -32.0f ? 0 : min(kFB - 1, (int)(__float_as_uint(-y) >> 18) - kFarBin0 + 1);
+    };
+    atomicAdd(&S.fcnt[far_bin(lt.x)], 1u);
+    atomicAdd(&S.fcnt[far_bin(lt.y)], 1u);
+    __syncthreads();
+    int pc[4], s4 = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pc[q] = (int)S.fcnt[4 * lane + q];
+      s4 += pc[q];
+    }
+    const int inc = wave_incl_scan_i(s4, lane);
+    const uint64_t bal = __ballot(inc >= k);
+    if (bal) {
+      const int lb = __ffsll((unsigned long long)bal) - 1;
+      int a = __builtin_amdgcn_readlane(inc - s4, lb), bs = 4 * lb + 3;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const int vq = __builtin_amdgcn_readlane(pc[q], lb);
+        if (a + vq >= k) {
+          bs = 4 * lb + q;
+          break;
+        }
+        a += vq;
+      }
+      if (bs < kFB - 1) {  // bin bs holds d < the bottom of bin bs + 1
+        flr = true;
+        Lm = bs == 0 ? -32.0f : -__uint_as_float((uint32_t)(bs + kFarBin0) << 18);
+      }
+    }
+  }
+  stamp(3);
+  if (flr) {
     // stage this wave's elements with y >= Lm, in index order (j, lane, element)
     uint64_t* seg = S.seg[wid];
     int run = 0;
@@ -1439,7 +1484,7 @@ void quad_sample_kernel(SampleParams P) {
   }
   __syncthreads();
   stamp(4);
-  if (bstar >= 0) {
+  if (flr) {
     int cq[NW], nw = 0;
     bool ovf = false;
 #pragma unroll
@@ -1462,12 +1507,12 @@ void quad_sample_kernel(SampleParams P) {
     }
   }
   const double Zr = wave_total<NW>([&](int q) { return wave_mass(S, q, m, c); });
-  if (!kon && row_topp_fast(R, S, m, c, Zr, p, bstar >= 0 ? Lm : -INFINITY, u, P.V, out)) {
+  if (!kon && row_topp_fast(R, S, m, c, Zr, p, Lm, u, P.V, out)) {
     stamp(5);
     stamp_path(kPathTopp);
     return;
   }
-  row_exact(R, S, m, c, Zr, kon, k, pon, p, bstar >= 0 ? Lm : -INFINITY, u, out);
+  row_exact(R, S, m, c, Zr, kon, k, pon, p, Lm, u, out);
   stamp(5);
   stamp_path(kPathExact);
 }

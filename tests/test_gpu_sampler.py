@@ -374,6 +374,39 @@ def test_streamed_rows_edge_cases(lsg, orc, dev, dtype, V):
     assert ids[8] % 5 != 0 and ids[10] == 12345
 
 
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 65536), (torch.float32, 65536), (torch.float32, 32768)])
+def test_far_topk_floor(lsg, orc, dev, dtype, V):
+    """B=320 top-k rows whose k-th largest logit lies far (up to thousands of
+    binary orders at T=0.05) below the maximum: Student-t(3) logits at low
+    temperature, k from 1 to past the lanes' pair maxima (1025, 4000), with
+    and without top-p; plus ties at the k-th value far below the maximum, a
+    crossing bin holding most of the row (window overflow: the exact path), a
+    maximum 1e30 above the rest (beyond the binned distances) and -inf
+    elements."""
+    g = torch.Generator(device=dev).manual_seed(V + 77)
+    B = 320
+    z = torch.randn(B, V, generator=g, device=dev)
+    chi = torch.randn(B, V, 3, generator=g, device=dev).pow(2).sum(-1)
+    x = 3.0 * z / torch.sqrt(chi / 3.0)
+    del z, chi
+    x[0, :] = -1000.0  # ties at the k-th value: 10 at 0, 50 at -500
+    x[0, torch.randperm(V, generator=g, device=dev)[:60]] = torch.tensor([0.0] * 10 + [-500.0] * 50, device=dev)
+    x[1, :] = torch.randn(V, generator=g, device=dev) * 1e-3  # k-th inside the bulk
+    x[1, 7] = 1000.0
+    x[2, 100] = 1e30  # distance beyond the last bin
+    x[3, ::3] = float("-inf")
+    x = x.to(dtype)
+    T = torch.tensor([0.8, 0.3, 0.05, 1.0], device=dev).repeat(B // 4)
+    K = torch.tensor([1, 2, 5, 40, 41, 200, 512, 1024, 1025, 4000], dtype=torch.int32,
+                     device=dev).repeat(B // 10)
+    P = torch.tensor([1.0, 1.0, 0.9, 1.0, 0.5], device=dev).repeat(B // 5)
+    T[0:4] = 0.8
+    K[0:4] = torch.tensor([20, 40, 40, 40], dtype=torch.int32, device=dev)
+    P[0:4] = 1.0
+    U = torch.rand(B, generator=g, device=dev)
+    check_sampling(lsg, orc, x, T, K, P, U, max_excused=2)
+
+
 def test_large_gather_and_count(lsg, orc, dev):
     """Large batch with row_idx (invalid entries -> -1) and a device row count
     below B_out: rows past the count stay untouched."""
