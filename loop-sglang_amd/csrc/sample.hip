@@ -49,6 +49,33 @@ constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
 // reference shifts (< 2^-17 relative per term).
 constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
 
+// Phase stamps, compiled in only by the profiling build (-DLSG_PHASE_STAMPS):
+// thread 0 of workgroup b writes the 100 MHz real-time counter at fixed points
+// of its row to g_row_stamps[b * 8 + slot] (slots: 0 kernel entry, 1 both
+// passes done (barrier 1), 2 candidate window staged, 3 dense path: histogram
+// done, 4 dense path: crossing bin gathered, 5 dense path: threshold known,
+// 7 threshold known on any path); slot 6 holds the hardware id (bits 0-31),
+// the XCC id (32-39) and the row's path (40-47: 1 unfiltered walk, 2 window of
+// at most 128, 3 ranked window, 4 dense top-p, 5 exact refinement, 6 argmax).
+constexpr int kRowStampSlots = 8, kRowStampRows = 8192;
+enum RowPath { kRowWalk = 1, kRowSmall = 2, kRowRanked = 3, kRowDense = 4, kRowRefine = 5, kRowArgmax = 6 };
+#ifdef LSG_PHASE_STAMPS
+__device__ unsigned long long g_row_stamps[kRowStampRows * kRowStampSlots];
+__device__ __forceinline__ void row_stamp_val(int slot, unsigned long long v) {
+  if (threadIdx.x == 0 && blockIdx.x < (unsigned)kRowStampRows) g_row_stamps[blockIdx.x * kRowStampSlots + slot] = v;
+}
+__device__ __forceinline__ void row_stamp(int slot) { row_stamp_val(slot, __builtin_amdgcn_s_memrealtime()); }
+__device__ __forceinline__ void row_stamp_path(int path) {
+  // HW_ID (hwreg 4: wave, SIMD, CU, SH, SE) and XCC_ID (hwreg 20)
+  const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+  const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xffu;
+  row_stamp_val(6, ((unsigned long long)path << 40) | ((unsigned long long)xcc << 32) | hw);
+}
+#else
+__device__ __forceinline__ void row_stamp(int) {}
+__device__ __forceinline__ void row_stamp_path(int) {}
+#endif
+
 // exp2 clamped to [0, 1]; the clamp folds into v_exp_f32 and maps NaN (from a
 // NaN logit) to 0.
 __device__ __forceinline__ float ex2c(float y) {
@@ -540,7 +567,7 @@ __device__ __forceinline__ float bin_floor(int b) { return -0.5f * (float)(b + 1
 // of the value in the high word, ~index in the low word).  Returns false when
 // the window does not reach the top-p mass (the exact search then decides).
 template <int NT>
-__device__ bool window_threshold(Smem<NT>& S, int nw, bool kon, int32_t k, bool pon, float p, double Z,
+__device__ __forceinline__ bool window_threshold(Smem<NT>& S, int nw, bool kon, int32_t k, bool pon, float p, double Z,
                                  const Ex& X, float* thr_out) {
   constexpr int NW = NT / kWave;
   const int t = threadIdx.x, wid = t >> 6;
@@ -1172,6 +1199,189 @@ __device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t l
   return fl;
 }
 
+// ---------------------------------------------------------------------------
+// Exact top-p of a row held in registers whose top-p set is too large for a
+// candidate window (near-flat rows keep thousands of elements):
+//   1. mass histogram of every member (element with y > -kDenseOrders) over
+//      bins of 1/kDenseRes binary order of y (float64 LDS atomics; a bin's
+//      sum depends on the order of the atomics only in its last bits, ~1e-13
+//      of the row mass), in the chunk-mass array;
+//   2. every wave scans it from the top: the bin b* where the mass reaches
+//      p * Z and the mass A above it (y is monotone in x, so the members above
+//      b* are exactly those with larger values);
+//   3. the members in b* (a few hundred, with few distinct values) are
+//      appended to LDS in one pass; wave 0 alone splits their key range into
+//      256 bins per level (2^-40 fixed-point masses, exact; its LDS operations
+//      stay in order, so no barrier) down to one key, the threshold;
+//   4. masses of the kept elements per register chunk, and the inverse CDF.
+// Each step costs a few instructions per element of the row (one compute unit
+// holds the row), so the passes read the register chunks directly.
+// Returns false (no state changed that the exact refinement relies on) when
+// the members do not reach p * Z or bin b* holds more than the staging area.
+// All waves call it together.
+// ---------------------------------------------------------------------------
+constexpr int kDenseRes = 32, kDenseOrders = 40;
+constexpr int kDenseBins = kDenseRes * kDenseOrders;  // 1280
+constexpr int kDensePL = kDenseBins / kWave;          // bins per lane in the scan
+
+template <typename T, int NT, int CAP, bool VEC, int FULL>
+__device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, double Z, float p, float u,
+                                           Smem<NT>& S, float* csum, int32_t* out) {
+  constexpr int EPV = Elem<T>::EPV, SH = KeyShift<T>::value;
+  constexpr int kCap = 2 * (NT / kWave) * Smem<NT>::kSeg;  // candidate keys staged (u32 view of S.stage)
+  static_assert(kDenseBins % (4 * kWave) == 0, "bins split evenly over the lanes, four at a time");
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  double* hist = reinterpret_cast<double*>(csum);
+  uint32_t* cand = reinterpret_cast<uint32_t*>(S.stage);
+  const float ylo = -(float)kDenseOrders;
+  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0.0;
+  if (t == 0) S.wn = 0;
+  __syncthreads();
+  // members: ylo < y <= 0, so bin = trunc(-32 y) lies in [0, kDenseBins)
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    if (R.has(j) && X.y(R.cm_at(j)) > ylo) {
+      uint4 v = R.d[j];
+      launder(v);
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        const float y = X.y(Elem<T>::get(v, i));
+        if (y > ylo) atomicAdd(&hist[(int)(-(float)kDenseRes * y)], (double)ex2c(y));
+      }
+    }
+  }
+  __syncthreads();
+  row_stamp(3);
+  // crossing bin, by every wave (lane l sums bins kDensePL*l ..)
+  const double target = (double)p * Z;
+  double ls = 0.0;
+#pragma unroll 1
+  for (int q = 0; q < kDensePL; q += 4) {
+    const double* h4 = hist + kDensePL * lane + q;
+    ls += (h4[0] + h4[1]) + (h4[2] + h4[3]);
+  }
+  const double incl = wave_incl_scan(ls, lane);
+  const uint64_t bal = __ballot(incl >= target);
+  if (!bal) return false;
+  const int lb = __ffsll((unsigned long long)bal) - 1;
+  double A = readlane_d(incl - ls, lb);
+  int bs = kDensePL * lb + kDensePL - 1;
+  for (int q = 0; q < kDensePL - 1; ++q) {
+    const double vq = hist[kDensePL * lb + q];
+    if (A + vq >= target) {
+      bs = kDensePL * lb + q;
+      break;
+    }
+    A += vq;
+  }
+  bs = uni(bs);
+  // members of bin bs (-(bs + 1)/32 < y <= -bs/32) -> cand, one LDS append per
+  // wave and element slot that holds any
+  const float yb = -(float)(bs + 1) / (float)kDenseRes, yt = -(float)bs / (float)kDenseRes;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    uint4 v = R.d[j];
+    launder(v);
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      const float x = Elem<T>::get(v, i);
+      const float y = X.y(x);
+      const bool in = R.has(j) && y > yb && y <= yt;
+      const uint64_t bm = __ballot(in);
+      if (bm) {
+        int b0 = 0;
+        if (lane == 0) b0 = atomicAdd(&S.wn, (int)__popcll(bm));
+        const int slot = __builtin_amdgcn_readlane(b0, 0) +
+                         (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+        if (in && slot < kCap) cand[slot] = okey(x);
+      }
+    }
+  }
+  __syncthreads();
+  row_stamp(4);
+  const int n = uni(S.wn);
+  if (n > kCap || n < 1) return false;
+  if (wid == 0) {
+    // the threshold key among the candidates: keys in [lo, hi), mass above hi
+    // (fixed point from here on)
+    const double tfix = target * kFix;
+    A *= kFix;
+    uint32_t kmn = 0xffffffffu, kmx = 0u;
+    for (int i = lane; i < n; i += kWave) {
+      const uint32_t kk = cand[i] >> SH;
+      kmn = min(kmn, kk);
+      kmx = max(kmx, kk);
+    }
+    uint32_t lo = (uint32_t)wave_min_i((int)(kmn ^ 0x80000000u)) ^ 0x80000000u;
+    uint32_t hi = ((uint32_t)wave_max_i((int)(kmx ^ 0x80000000u)) ^ 0x80000000u) + 1u;
+    unsigned long long* bins = S.rbins[0];
+    uint32_t tk = lo;
+#pragma unroll 1
+    for (int level = 0; level < 8 && hi - lo > 1u; ++level) {
+      int sh = 0;
+      while (((hi - lo - 1u) >> sh) >= (uint32_t)kRefBins) ++sh;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bins[4 * lane + q] = 0ull;
+      for (int i = lane; i < n; i += kWave) {
+        const uint32_t kx = cand[i];
+        const uint32_t kk = kx >> SH;
+        if (kk >= lo && kk < hi) atomicAdd(&bins[(hi - 1u - kk) >> sh], fix40(X.e(okey_inv(kx))));
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS atomics are done
+      double bv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[q] = (double)bins[4 * lane + q];
+      const double bl = (bv[0] + bv[1]) + (bv[2] + bv[3]);
+      const double binc = wave_incl_scan(bl, lane);
+      const uint64_t bb = __ballot(A + binc >= tfix);
+      if (!bb) {  // rounding of the bin sums: keep the whole bracket
+        tk = lo;
+        break;
+      }
+      const int lq = __ffsll((unsigned long long)bb) - 1;
+      double acc = A + readlane_d(binc - bl, lq);
+      int b2 = 4 * lq + 3;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const double vq = readlane_d(bv[q], lq);
+        if (acc + vq >= tfix) {
+          b2 = 4 * lq + q;
+          break;
+        }
+        acc += vq;
+      }
+      A = acc;
+      const uint32_t nhi = hi - ((uint32_t)b2 << sh);
+      lo = nhi - lo > (1u << sh) ? nhi - (1u << sh) : lo;
+      hi = nhi;
+      tk = lo;
+    }
+    if (lane == 0) S.pick = (int)tk;
+  }
+  __syncthreads();
+  row_stamp(5);
+  row_stamp(7);
+  row_stamp_path(kRowDense);
+  const float thr = okey_inv((uint32_t)S.pick << SH);
+  // kept masses per register chunk (the histogram is no longer read)
+  float* cs = csum + t;
+  double tmass = 0.0;
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    float sj = 0.0f;
+    if (R.has(j) && R.cm_at(j) >= thr) {
+      uint4 v = R.d[j];
+      launder(v);
+      sj = esum_chunk_ge<T>(v, X, thr);
+    }
+    cs[j * NT] = sj;
+    tmass += (double)sj;
+  }
+  cdf_walk<true>(R, tmass, cs, [&](int) { return 0.0f; }, [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, u, S,
+                 out);
+  return true;
+}
+
 template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, const RowArgs& A, int32_t* out,
                                                  Smem<NT>& S, float* csum) {
@@ -1245,12 +1455,15 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
   }
   __syncthreads();
+  row_stamp(1);
   // The rest of the row is short, latency-bound work: let it go ahead of the
   // co-resident workgroup's streaming passes.
   __builtin_amdgcn_s_setprio(2);
   const float gm = lds_max<NW>(S.wmax);
   if (!tvalid || !(gm > -INFINITY) || !(gm < INFINITY)) {
     const int32_t id = row_argmax<NW, T>(R, tm, gm, S.red);
+    row_stamp(7);
+    row_stamp_path(kRowArgmax);
     if (t == 0) *out = id;
     return;
   }
@@ -1271,6 +1484,8 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   };
 
   if (!kon && !pon) {
+    row_stamp(7);
+    row_stamp_path(kRowWalk);
     wave_refs();
     int wstar;
     double base;
@@ -1399,6 +1614,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     S.wcnt[wid] = 0;
   }
   __syncthreads();
+  row_stamp(2);
   // window size, segment bases (lane q < NW) and overflow of a segment
   const int cq = lane < NW ? S.wcnt[lane] : 0;
   const int bq_incl = wave_incl_scan_i(cq, lane);
@@ -1469,6 +1685,8 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     }
     uint32_t tkey;
     if (!window_pick(in, kx, em, cnt, pre, nw, kon, A.k, pon, A.p, Z, &tkey)) tkey = 0u;  // unreachable
+    row_stamp(7);
+    row_stamp_path(kRowSmall);
     // inverse CDF over the kept entries (key >= tkey), in index order: slot 0
     // of lanes 0..63, then slot 1
     float ek[2];
@@ -1516,6 +1734,8 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   if (bin >= 0 && nw <= Smem<NT>::kWin && !ovf) {
     float thr;
     if (window_threshold<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &thr)) {
+      row_stamp(7);
+      row_stamp_path(kRowRanked);
       tmass = masked_masses(R, X, thr, cs);
       cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; },
                       [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, A.u, S, out);
@@ -1527,6 +1747,11 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   // top-p every element with mass at least 2^-40 of the maximum: below that,
   // the whole rest of the row weighs less than 2^-24 of Z, so a boundary there
   // is within the parity tolerance whichever way it falls.
+  // (rows of up to six register chunks per thread: with more, the chunks and
+  // the path's state exceed the 64 registers of a two-workgroup CU)
+  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(unsigned long long)) {
+    if (!kon && dense_topp(R, X, Z, A.p, A.u, S, csum, out)) return;
+  }
   const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
                                 : (kon ? (okey(-INFINITY) >> SH) : (okey(x_at_least(X, -40.0f)) >> SH));
   uint32_t tk = 0;
@@ -1545,6 +1770,8 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     ok = refine_threshold<NT, T>(R, X, Z, false, 0, A.p, klo, S, &tk);
   }
   const float thr = ok ? okey_inv(tk << SH) : select_exact<NW, T>(R, X, Z, kon, A.k, pon, A.p, S.red);
+  row_stamp(7);
+  row_stamp_path(kRowRefine);
   tmass = masked_masses(R, X, thr, cs);
   cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; }, [&](float x) { return x >= thr ? X.e(x) : 0.0f; },
                   A.u, S, out);
@@ -1557,7 +1784,7 @@ template <bool GREEDY, typename T, int NT, int CAP, bool VEC, int FULL, int WPE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE, 8)))
 void sampler_kernel(SampleParams P) {
   __shared__ Smem<NT> S;
-  __shared__ float csum[GREEDY ? 1 : NT * CAP];  // chunk masses, [j][thread]
+  __shared__ __align__(16) float csum[GREEDY ? 1 : NT * CAP];  // chunk masses, [j][thread]
   __shared__ uint32_t cmax[NT * Row<T, NT, CAP, VEC, FULL>::kCmWords];  // chunk maxima, [thread][j]
   int64_t nrows = P.B_out;
   if (P.n_rows_dev) nrows = min(nrows, (int64_t)uni(*P.n_rows_dev));
@@ -1571,6 +1798,7 @@ void sampler_kernel(SampleParams P) {
   // The arguments' loads go out before the row's and are made wave-uniform
   // after it: converting right away would wait a full memory round trip
   // before the row is requested.
+  row_stamp(0);
   RowArgs A{};
   if (!GREEDY) A = row_args_load(P, r);
   Row<T, NT, CAP, VEC, FULL> R;
@@ -1658,3 +1886,11 @@ extern "C" int lsg_sample(const void* logits, int dtype, int64_t B_src, int64_t 
   if (rc != LSG_OK) return rc;
   return check_launch("lsg_sample");
 }
+
+#ifdef LSG_PHASE_STAMPS
+// Copies the phase stamps of the one-row-per-workgroup sampler's last launch.
+extern "C" int lsg_row_stamps_read(void* dst, size_t bytes) {
+  const size_t n = sizeof(lsg::g_row_stamps);
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(lsg::g_row_stamps), bytes < n ? bytes : n, 0, hipMemcpyDeviceToHost);
+}
+#endif

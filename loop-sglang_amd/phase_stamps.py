@@ -6,8 +6,9 @@ then, on the GPU:
     python loop-sglang_amd/phase_stamps.py [--workload sample_huginn] [--nbuf 5]
 
 The profiling build (libloopsgl_tok_stamps.so, -DLSG_PHASE_STAMPS) has thread 0
-of every workgroup of the four-wave row sampler write the 100 MHz real-time
-counter at six points of its row (start, wave 0's pass done, barrier 1 passed,
+of every workgroup of the streamed-row sampler (or, for batches of no more rows
+than compute units, of the one-row-per-workgroup sampler) write the 100 MHz
+real-time counter at fixed points of its row (start, wave 0's pass done, barrier 1 passed,
 floor known, candidates staged, end), its hardware/XCC ids and the path the row
 took.  The script rotates `nbuf` logits buffers (so the timed launch reads from
 HBM, not from the Infinity Cache), times eager launches, then reads the stamps
@@ -28,6 +29,34 @@ ROOT = os.path.dirname(HERE)
 SLOTS, ROWS = 8, 8192
 PATHS = {1: "window", 2: "two-pass top-p", 3: "exact refinement", 4: "unfiltered walk", 5: "argmax",
          6: "small window"}
+# the one-row-per-workgroup sampler (batches of no more rows than compute units)
+ROW_PATHS = {1: "unfiltered walk", 2: "window <= 128", 3: "ranked window", 4: "dense top-p", 5: "exact refinement",
+             6: "argmax"}
+
+
+def row_sampler_table(st, B):
+    """Phases of the one-row-per-workgroup sampler (slots: 0 entry, 1 passes
+    done, 2 window staged, 3-5 dense path: histogram, gather, threshold,
+    7 threshold known, 6 ids and path)."""
+    info = st[:, 6]
+    path_of = (info >> 40) & 0xFF
+    base = st[:, 0].min()
+    rel = (st - base) * 0.01
+    have = lambda c: st[:, c] > 0
+    pct = lambda v: "p50 %6.2f  p90 %6.2f  max %6.2f" % (np.median(v), np.percentile(v, 90), v.max())
+    print("kernel entry (rel. first):", pct(rel[:, 0]))
+    print("threshold known (rel. first):", pct(rel[have(7), 7]))
+    for name, c0, c1 in [("entry -> passes done", 0, 1), ("passes done -> window staged", 1, 2),
+                         ("window staged -> threshold", 2, 7), ("dense: staged -> histogram", 2, 3),
+                         ("dense: histogram -> gathered", 3, 4), ("dense: gathered -> threshold", 4, 5)]:
+        ok = have(c0) & have(c1) & (st[:, c1] >= st[:, c0])
+        if ok.any():
+            print(f"{name:34s} ({ok.sum():4d} rows): {pct(rel[ok, c1] - rel[ok, c0])}")
+    for code in sorted(set(path_of.tolist())):
+        sel = (path_of == code) & have(7)
+        if sel.any():
+            print(f"path {ROW_PATHS.get(code, code)!s:18s}: {sel.sum():4d} rows, entry -> threshold "
+                  f"{pct(rel[sel, 7] - rel[sel, 0])}")
 
 
 def main():
@@ -35,6 +64,8 @@ def main():
     ap.add_argument("--workload", default="sample_huginn", choices=["sample_huginn", "sample_ouro", "cdb_mixed_depth"])
     ap.add_argument("--nbuf", type=int, default=5)
     ap.add_argument("--launches", type=int, default=20)
+    ap.add_argument("--lib", default=os.path.join(HERE, "libloopsgl_tok_stamps.so"),
+                    help="profiling library (a -DLSG_PHASE_STAMPS build)")
     a = ap.parse_args()
     sys.path.insert(0, ROOT)
     import torch
@@ -42,7 +73,7 @@ def main():
     import __graft_entry__
 
     pkg = __graft_entry__.package()
-    path = os.path.join(HERE, "libloopsgl_tok_stamps.so")
+    path = a.lib
     if not os.path.exists(path):
         raise SystemExit(f"{path} missing: run python loop-sglang_amd/build.py --stamps first")
     pkg._lib.use_library(path)
@@ -69,6 +100,13 @@ def main():
     pkg.sample_rows(bufs[(a.launches + 1) % a.nbuf], *args)
     torch.cuda.synchronize()
     raw = np.zeros(ROWS * SLOTS, dtype=np.uint64)
+    if B <= torch.cuda.get_device_properties(dev).multi_processor_count:
+        L.lsg_row_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+        L.lsg_row_stamps_read.restype = ctypes.c_int
+        if L.lsg_row_stamps_read(raw.ctypes.data, raw.nbytes) != 0:
+            raise SystemExit("lsg_row_stamps_read failed")
+        row_sampler_table(raw.reshape(ROWS, SLOTS)[:B].astype(np.int64), B)
+        return
     if L.lsg_phase_stamps_read(raw.ctypes.data, raw.nbytes) != 0:
         raise SystemExit("lsg_phase_stamps_read failed")
     st = raw.reshape(ROWS, SLOTS)[:min(B, ROWS)].astype(np.int64)

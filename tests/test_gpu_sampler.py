@@ -162,6 +162,37 @@ def test_flat_rows_exact_path(lsg, orc, dev):
     check_sampling(lsg, orc, x, T, K, P, U, max_excused=1)
 
 
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 49152), (torch.float16, 49152), (torch.float32, 24576)])
+def test_dense_topp_rows(lsg, orc, dev, dtype, V):
+    """Top-p rows whose kept set holds thousands of elements (B=64 <= CUs:
+    one row per CU, six register chunks per thread): the mass histogram, the
+    crossing bin's members and their key radix.  Rows: near-flat Gaussian at
+    several T and p (0.05 .. 0.999), thresholds near x = 0 (wide key span in
+    the crossing bin), NaN and -inf elements, half the row tied at one value,
+    a constant row (every element in one bin: the exact refinement decides),
+    and a row with a single dominant element."""
+    g = torch.Generator(device=dev).manual_seed(V + 5)
+    B = 64
+    x = torch.randn(B, V, generator=g, device=dev) * 0.9
+    x[1] -= x[1].mean() + 3.0 * x[1].std()  # most of the row far below its top
+    x[2, ::7] = float("nan")
+    x[3, ::5] = float("-inf")
+    x[4, : V // 2] = 0.5  # half the row tied
+    x[5, :] = 1.25  # constant
+    x[6, 123] = 40.0  # one dominant element
+    x[7] = torch.randn(V, generator=g, device=dev) * 0.01  # values packed around 0
+    x = x.to(dtype)
+    T = torch.tensor([0.3, 0.7, 1.0, 1.5], device=dev).repeat(B // 4)
+    P = torch.tensor([0.05, 0.5, 0.8, 0.9, 0.95, 0.99, 0.999, 0.7], device=dev).repeat(B // 8)
+    U = torch.rand(B, generator=g, device=dev)
+    # near-flat rows: each element carries ~1/30000 of the mass, so a few
+    # percent of the rows have u or p within 1e-6 of a CDF step
+    check_sampling(lsg, orc, x, T, None, P, U, max_excused=12)
+    K = torch.full((B,), V, dtype=torch.int32, device=dev)
+    K[::9] = 1000  # top-k + top-p rows keep the previous paths
+    check_sampling(lsg, orc, x, T, K, P, U, max_excused=12)
+
+
 def test_closed_forms_gpu(lsg, dev):
     """Uniform row -> floor(u V); one-hot -> hot index; T <= 0 -> argmax;
     all -inf -> 0; +inf max -> first +inf (argmax rule)."""
