@@ -53,11 +53,12 @@ constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
 // thread 0 of workgroup b writes the 100 MHz real-time counter at fixed points
 // of its row to g_row_stamps[b * 8 + slot] (slots: 0 kernel entry, 1 both
 // passes done (barrier 1), 2 candidate window staged, 3 dense path: histogram
-// done, 4 dense path: crossing bin gathered, 5 dense path: threshold known,
-// 7 threshold known on any path); slot 6 holds the hardware id (bits 0-31),
+// done, 4 dense path: crossing bracketed, 5 dense path: bracket gathered,
+// 7 threshold known on any path, 8 id written, by the lane writing it); slot 6
+// holds the hardware id (bits 0-31),
 // the XCC id (32-39) and the row's path (40-47: 1 unfiltered walk, 2 window of
 // at most 128, 3 ranked window, 4 dense top-p, 5 exact refinement, 6 argmax).
-constexpr int kRowStampSlots = 8, kRowStampRows = 8192;
+constexpr int kRowStampSlots = 16, kRowStampRows = 8192;
 enum RowPath { kRowWalk = 1, kRowSmall = 2, kRowRanked = 3, kRowDense = 4, kRowRefine = 5, kRowArgmax = 6 };
 #ifdef LSG_PHASE_STAMPS
 __device__ unsigned long long g_row_stamps[kRowStampRows * kRowStampSlots];
@@ -65,6 +66,10 @@ __device__ __forceinline__ void row_stamp_val(int slot, unsigned long long v) {
   if (threadIdx.x == 0 && blockIdx.x < (unsigned)kRowStampRows) g_row_stamps[blockIdx.x * kRowStampSlots + slot] = v;
 }
 __device__ __forceinline__ void row_stamp(int slot) { row_stamp_val(slot, __builtin_amdgcn_s_memrealtime()); }
+__device__ __forceinline__ void row_stamp_end() {
+  if (blockIdx.x < (unsigned)kRowStampRows)
+    g_row_stamps[blockIdx.x * kRowStampSlots + 8] = __builtin_amdgcn_s_memrealtime();
+}
 __device__ __forceinline__ void row_stamp_path(int path) {
   // HW_ID (hwreg 4: wave, SIMD, CU, SH, SE) and XCC_ID (hwreg 20)
   const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
@@ -73,6 +78,7 @@ __device__ __forceinline__ void row_stamp_path(int path) {
 }
 #else
 __device__ __forceinline__ void row_stamp(int) {}
+__device__ __forceinline__ void row_stamp_end() {}
 __device__ __forceinline__ void row_stamp_path(int) {}
 #endif
 
@@ -878,6 +884,7 @@ __device__ __forceinline__ void wave_walk(Row<T, NT, CAP, VEC, FULL>& R, const f
   }
   if (pick < 0) pick = lastpos < 0 ? 0 : lastpos;
   *out = (int32_t)R.elem_index(jstar, pick);
+  row_stamp_end();
 }
 
 // The crossing wave of U = u * (sum of the wave masses sw, one per lane < NW):
@@ -1201,43 +1208,52 @@ __device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t l
 
 // ---------------------------------------------------------------------------
 // Exact top-p of a row held in registers whose top-p set is too large for a
-// candidate window (near-flat rows keep thousands of elements):
-//   1. mass histogram of every member (element with y > -kDenseOrders) over
-//      bins of 1/kDenseRes binary order of y (float64 LDS atomics; a bin's
-//      sum depends on the order of the atomics only in its last bits, ~1e-13
-//      of the row mass), in the chunk-mass array;
-//   2. every wave scans it from the top: the bin b* where the mass reaches
-//      p * Z and the mass A above it (y is monotone in x, so the members above
-//      b* are exactly those with larger values);
-//   3. the members in b* (a few hundred, with few distinct values) are
-//      appended to LDS in one pass; wave 0 alone splits their key range into
-//      256 bins per level (2^-40 fixed-point masses, exact; its LDS operations
-//      stay in order, so no barrier) down to one key, the threshold;
-//   4. masses of the kept elements per register chunk, and the inverse CDF.
-// Each step costs a few instructions per element of the row (one compute unit
-// holds the row), so the passes read the register chunks directly.
-// Returns false (no state changed that the exact refinement relies on) when
-// the members do not reach p * Z or bin b* holds more than the staging area.
-// All waves call it together.
+// candidate window (near-flat rows keep thousands of elements).  One compute
+// unit holds the row, so every full pass costs a few microseconds; the path
+// makes two:
+//   1. a count histogram of the members (elements with y > -32) over bins of
+//      1/128 binary order of y (one LDS add per element, no exponential).
+//      Every element of bin b weighs within a factor 2^(1/256) of
+//      2^(-(b + 1/2)/128), and over a bin the errors largely cancel, so the
+//      exact crossing of p * Z lies, but for rows with masses piled at bin
+//      edges, between the first bins where the estimate reaches
+//      p * Z (1 -+ 2^-12) (a block scan, every thread holding four bins);
+//   2. one pass over the register chunks: each chunk's mass above the bracket
+//      (the float sums the inverse CDF uses) to the chunk-mass array, and the
+//      members inside the bracket to per-wave LDS segments (a wave-uniform
+//      count, no atomics), their positions kept in a bit mask;
+//   3. wave 0 checks that the mass above the bracket is below p * Z and that
+//      the bracket's members reach it, then splits their key range into 256
+//      bins per level (2^-40 fixed-point masses, exact; one wave, so no
+//      barrier) down to one key, the threshold;
+//   4. the kept masses per chunk are the masses above the bracket plus the
+//      kept members (a few per thread), and the inverse CDF walks them.
+// Returns false (the exact refinement then decides; nothing it relies on has
+// changed) when the bracket misses the crossing or a segment overflows.
+// Every wave calls it together.
 // ---------------------------------------------------------------------------
-constexpr int kDenseRes = 32, kDenseOrders = 40;
-constexpr int kDenseBins = kDenseRes * kDenseOrders;  // 1280
-constexpr int kDensePL = kDenseBins / kWave;          // bins per lane in the scan
+constexpr int kDenseRes = 128, kDenseOrders = 32;
+constexpr int kDenseBins = kDenseRes * kDenseOrders;  // 4096
 
 template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, double Z, float p, float u,
                                            Smem<NT>& S, float* csum, int32_t* out) {
-  constexpr int EPV = Elem<T>::EPV, SH = KeyShift<T>::value;
-  constexpr int kCap = 2 * (NT / kWave) * Smem<NT>::kSeg;  // candidate keys staged (u32 view of S.stage)
-  static_assert(kDenseBins % (4 * kWave) == 0, "bins split evenly over the lanes, four at a time");
+  constexpr int EPV = Elem<T>::EPV, SH = KeyShift<T>::value, NW = NT / kWave;
+  constexpr int kSegC = 2 * Smem<NT>::kSeg;     // candidate keys per wave (u32 view of S.stage)
+  static_assert(kSegC % kWave == 0, "segments hold whole rounds of a wave");
+  constexpr int BPT = kDenseBins / NT;           // bins per thread in the scan
+  static_assert(BPT * NT == kDenseBins && BPT >= 1, "bins split evenly over the threads");
+  static_assert(CAP * EPV <= 64, "member positions fit one 64-bit mask");
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  double* hist = reinterpret_cast<double*>(csum);
-  uint32_t* cand = reinterpret_cast<uint32_t*>(S.stage);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(csum);
   const float ylo = -(float)kDenseOrders;
-  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0.0;
-  if (t == 0) S.wn = 0;
+  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0u;
+  if (t == 0) {
+    S.rbin = -1;                 // bracket top bin (none yet)
+    S.pick = kDenseBins - 1;     // bracket bottom bin
+  }
   __syncthreads();
-  // members: ylo < y <= 0, so bin = trunc(-32 y) lies in [0, kDenseBins)
+  // members: ylo < y <= 0, so bin = trunc(-128 y) lies in [0, kDenseBins)
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
     if (R.has(j) && X.y(R.cm_at(j)) > ylo) {
@@ -1246,100 +1262,158 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
 #pragma unroll
       for (int i = 0; i < EPV; ++i) {
         const float y = X.y(Elem<T>::get(v, i));
-        if (y > ylo) atomicAdd(&hist[(int)(-(float)kDenseRes * y)], (double)ex2c(y));
+        if (y > ylo) atomicAdd(&hist[(int)(-(float)kDenseRes * y)], 1u);
       }
     }
   }
   __syncthreads();
   row_stamp(3);
-  // crossing bin, by every wave (lane l sums bins kDensePL*l ..)
+  // block scan of the estimates (thread t: bins BPT*t ..)
   const double target = (double)p * Z;
-  double ls = 0.0;
-#pragma unroll 1
-  for (int q = 0; q < kDensePL; q += 4) {
-    const double* h4 = hist + kDensePL * lane + q;
-    ls += (h4[0] + h4[1]) + (h4[2] + h4[3]);
-  }
-  const double incl = wave_incl_scan(ls, lane);
-  const uint64_t bal = __ballot(incl >= target);
-  if (!bal) return false;
-  const int lb = __ffsll((unsigned long long)bal) - 1;
-  double A = readlane_d(incl - ls, lb);
-  int bs = kDensePL * lb + kDensePL - 1;
-  for (int q = 0; q < kDensePL - 1; ++q) {
-    const double vq = hist[kDensePL * lb + q];
-    if (A + vq >= target) {
-      bs = kDensePL * lb + q;
-      break;
+  const double tL = target * (1.0 - 1.0 / 4096.0), tU = target * (1.0 + 1.0 / 4096.0);
+  float est[BPT];
+  {
+    const float r1 = 0.99459839f;  // 2^(-1/128)
+    float f = ex2c(-((float)(BPT * t) + 0.5f) / (float)kDenseRes);
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      est[q] = (float)hist[BPT * t + q] * f;
+      f *= r1;
     }
-    A += vq;
   }
-  bs = uni(bs);
-  // members of bin bs (-(bs + 1)/32 < y <= -bs/32) -> cand, one LDS append per
-  // wave and element slot that holds any
-  const float yb = -(float)(bs + 1) / (float)kDenseRes, yt = -(float)bs / (float)kDenseRes;
+  float ts = 0.0f;
 #pragma unroll
-  for (int j = 0; j < CAP; ++j) {
-    uint4 v = R.d[j];
-    launder(v);
+  for (int q = 0; q < BPT; ++q) ts += est[q];
+  const double wi = wave_incl_scan((double)ts, lane);
+  if (lane == kWave - 1) S.red[wid] = wi;
+  __syncthreads();  // every wave has read the histogram: the chunk-mass array is free
+  {
+    double base = 0.0;
+    for (int q = 0; q < wid; ++q) base += S.red[q];
+    double c = base + wi - (double)ts;  // estimate above bin BPT*t
 #pragma unroll
-    for (int i = 0; i < EPV; ++i) {
-      const float x = Elem<T>::get(v, i);
-      const float y = X.y(x);
-      const bool in = R.has(j) && y > yb && y <= yt;
-      const uint64_t bm = __ballot(in);
-      if (bm) {
-        int b0 = 0;
-        if (lane == 0) b0 = atomicAdd(&S.wn, (int)__popcll(bm));
-        const int slot = __builtin_amdgcn_readlane(b0, 0) +
-                         (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
-        if (in && slot < kCap) cand[slot] = okey(x);
-      }
+    for (int q = 0; q < BPT; ++q) {
+      const double cn = c + (double)est[q];
+      if (c < tL && cn >= tL) S.rbin = BPT * t + q;
+      if (c < tU && cn >= tU) S.pick = BPT * t + q;
+      c = cn;
     }
   }
   __syncthreads();
   row_stamp(4);
-  const int n = uni(S.wn);
-  if (n > kCap || n < 1) return false;
-  if (wid == 0) {
-    // the threshold key among the candidates: keys in [lo, hi), mass above hi
-    // (fixed point from here on)
-    const double tfix = target * kFix;
-    A *= kFix;
-    uint32_t kmn = 0xffffffffu, kmx = 0u;
-    for (int i = lane; i < n; i += kWave) {
-      const uint32_t kk = cand[i] >> SH;
-      kmn = min(kmn, kk);
-      kmx = max(kmx, kk);
+  const int b0 = uni(S.rbin), b1 = uni(S.pick);
+  if (b0 < 0) return false;
+  // the bracket: bins [b0, b1], i.e. yb < y <= yt
+  const float yt = -(float)b0 / (float)kDenseRes;
+  const float yb = b1 == kDenseBins - 1 ? ylo : -(float)(b1 + 1) / (float)kDenseRes;
+  // one pass: chunk masses above the bracket (to the chunk-mass array),
+  // members inside it (to this wave's segment)
+  uint32_t* seg = reinterpret_cast<uint32_t*>(S.stage) + wid * kSegC;
+  // the candidate list: refinement bin copies 1-3 (wave 0 bins with copy 0)
+  uint32_t* list = reinterpret_cast<uint32_t*>(S.rbins[1]);
+  constexpr int kList = (int)(3 * (kRefBins + 1) * sizeof(unsigned long long) / sizeof(uint32_t));
+  int run = 0;
+  float* cs = csum + t;
+  double above = 0.0;
+  uint64_t inm = 0ull;  // bit j * EPV + i: element i of chunk j lies in the bracket
+#pragma unroll
+  for (int j = 0; j < CAP; ++j) {
+    uint4 v = R.d[j];
+    launder(v);
+    float e[EPV];
+    uint32_t mj = 0u;
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      const float x = Elem<T>::get(v, i);
+      const float y = X.y(x);
+      e[i] = R.has(j) && y > yt ? ex2c(y) : 0.0f;
+      const bool in = R.has(j) && y > yb && y <= yt;
+      mj |= in ? (1u << i) : 0u;
+      const uint64_t bm = __ballot(in);
+      if (bm) {
+        const int slot = run + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+        if (in && slot < kSegC) seg[slot] = okey(x);
+        run += (int)__popcll(bm);
+      }
     }
+    inm |= (uint64_t)mj << (j * EPV);
+    const float cj = tree_sum<EPV>(e);
+    cs[j * NT] = cj;
+    above += (double)cj;
+  }
+  above = wave_sum(above);
+  if (lane == 0) {
+    S.wtot[wid] = above;
+    S.wcnt[wid] = run;
+  }
+  __syncthreads();
+  row_stamp(5);
+  int n = 0;
+  bool ovf = false;
+  double A = 0.0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    const int cq = S.wcnt[q];
+    n += cq;
+    ovf = ovf || cq > kSegC;
+    A += S.wtot[q];
+  }
+  if (ovf || n < 1 || n > kList || !(A < target)) return false;
+  // the segments -> one list (in the refinement bins' spare copies)
+  {
+    int pre = 0;
+    for (int q = 0; q < wid; ++q) pre += S.wcnt[q];
+#pragma unroll
+    for (int r = 0; r < kSegC / kWave; ++r) {
+      const int sl = r * kWave + lane;
+      if (sl < run) list[pre + sl] = seg[sl];
+    }
+  }
+  __syncthreads();
+  auto each_cand = [&](auto&& f) {
+    for (int i = lane; i < n; i += kWave) f(list[i]);
+  };
+  if (wid == 0) {
+    // the threshold key among the candidates: keys in [lo, hi), fixed-point
+    // mass above hi
+    const double tfix = target * kFix;
+    double Af = A * kFix;
+    uint32_t kmn = 0xffffffffu, kmx = 0u;
+    double tot = 0.0;
+    each_cand([&](uint32_t kx) {
+      kmn = min(kmn, kx >> SH);
+      kmx = max(kmx, kx >> SH);
+      tot += (double)fix40(X.e(okey_inv(kx)));
+    });
     uint32_t lo = (uint32_t)wave_min_i((int)(kmn ^ 0x80000000u)) ^ 0x80000000u;
     uint32_t hi = ((uint32_t)wave_max_i((int)(kmx ^ 0x80000000u)) ^ 0x80000000u) + 1u;
-    unsigned long long* bins = S.rbins[0];
+    const int found = Af + wave_sum(tot) >= tfix ? 1 : 0;  // the bracket's members reach p * Z
     uint32_t tk = lo;
+    unsigned long long* bins = S.rbins[0];
 #pragma unroll 1
-    for (int level = 0; level < 8 && hi - lo > 1u; ++level) {
+    for (int level = 0; level < 8 && found && hi - lo > 1u; ++level) {
       int sh = 0;
       while (((hi - lo - 1u) >> sh) >= (uint32_t)kRefBins) ++sh;
 #pragma unroll
       for (int q = 0; q < 4; ++q) bins[4 * lane + q] = 0ull;
-      for (int i = lane; i < n; i += kWave) {
-        const uint32_t kx = cand[i];
+      each_cand([&](uint32_t kx) {
         const uint32_t kk = kx >> SH;
         if (kk >= lo && kk < hi) atomicAdd(&bins[(hi - 1u - kk) >> sh], fix40(X.e(okey_inv(kx))));
-      }
+      });
       __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS atomics are done
       double bv[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) bv[q] = (double)bins[4 * lane + q];
       const double bl = (bv[0] + bv[1]) + (bv[2] + bv[3]);
       const double binc = wave_incl_scan(bl, lane);
-      const uint64_t bb = __ballot(A + binc >= tfix);
+      const uint64_t bb = __ballot(Af + binc >= tfix);
       if (!bb) {  // rounding of the bin sums: keep the whole bracket
         tk = lo;
         break;
       }
       const int lq = __ffsll((unsigned long long)bb) - 1;
-      double acc = A + readlane_d(binc - bl, lq);
+      double acc = Af + readlane_d(binc - bl, lq);
       int b2 = 4 * lq + 3;
 #pragma unroll
       for (int q = 0; q < 3; ++q) {
@@ -1350,32 +1424,37 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
         }
         acc += vq;
       }
-      A = acc;
+      Af = acc;
       const uint32_t nhi = hi - ((uint32_t)b2 << sh);
       lo = nhi - lo > (1u << sh) ? nhi - (1u << sh) : lo;
       hi = nhi;
       tk = lo;
     }
-    if (lane == 0) S.pick = (int)tk;
+    if (lane == 0) {
+      S.pick = (int)tk;
+      S.rbin = found;
+    }
   }
   __syncthreads();
-  row_stamp(5);
+  if (!S.rbin) return false;
   row_stamp(7);
   row_stamp_path(kRowDense);
   const float thr = okey_inv((uint32_t)S.pick << SH);
-  // kept masses per register chunk (the histogram is no longer read)
-  float* cs = csum + t;
+  // kept masses per register chunk: above the bracket, plus the kept members
   double tmass = 0.0;
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
-    float sj = 0.0f;
-    if (R.has(j) && R.cm_at(j) >= thr) {
-      uint4 v = R.d[j];
-      launder(v);
-      sj = esum_chunk_ge<T>(v, X, thr);
+    uint32_t mb = (uint32_t)(inm >> (j * EPV)) & ((1u << EPV) - 1u);
+    float cj = cs[j * NT];
+    if (mb) {
+      const uint4 v = R.d[j];
+      for (; mb; mb &= mb - 1u) {
+        const float x = Elem<T>::get(v, __builtin_ctz(mb));
+        if (x >= thr) cj += X.e(x);
+      }
+      cs[j * NT] = cj;
     }
-    cs[j * NT] = sj;
-    tmass += (double)sj;
+    tmass += (double)cj;
   }
   cdf_walk<true>(R, tmass, cs, [&](int) { return 0.0f; }, [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, u, S,
                  out);
@@ -1715,7 +1794,10 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     else if (k1) src = 63 - __clzll((long long)k1), h = 1;
     else if (k0) src = 63 - __clzll((long long)k0);
     const int id = __builtin_amdgcn_readlane(h ? idx[1] : idx[0], src);
-    if (lane == 0) *out = id;
+    if (lane == 0) {
+      *out = id;
+      row_stamp_end();
+    }
     return;
   }
   if (bin >= 0 && nw <= Smem<NT>::kWin && !ovf) {
@@ -1749,7 +1831,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   // is within the parity tolerance whichever way it falls.
   // (rows of up to six register chunks per thread: with more, the chunks and
   // the path's state exceed the 64 registers of a two-workgroup CU)
-  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(unsigned long long)) {
+  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(uint32_t)) {
     if (!kon && dense_topp(R, X, Z, A.p, A.u, S, csum, out)) return;
   }
   const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)

@@ -34,10 +34,13 @@ ROW_PATHS = {1: "unfiltered walk", 2: "window <= 128", 3: "ranked window", 4: "d
              6: "argmax"}
 
 
+ROW_SLOTS = 16
+
+
 def row_sampler_table(st, B):
     """Phases of the one-row-per-workgroup sampler (slots: 0 entry, 1 passes
-    done, 2 window staged, 3-5 dense path: histogram, gather, threshold,
-    7 threshold known, 6 ids and path)."""
+    done, 2 window staged, 3-5 dense path: histogram, bracket, gather,
+    7 threshold known, 8 id written, 6 ids and path)."""
     info = st[:, 6]
     path_of = (info >> 40) & 0xFF
     base = st[:, 0].min()
@@ -46,9 +49,11 @@ def row_sampler_table(st, B):
     pct = lambda v: "p50 %6.2f  p90 %6.2f  max %6.2f" % (np.median(v), np.percentile(v, 90), v.max())
     print("kernel entry (rel. first):", pct(rel[:, 0]))
     print("threshold known (rel. first):", pct(rel[have(7), 7]))
+    print("id written (rel. first):", pct(rel[have(8), 8]))
     for name, c0, c1 in [("entry -> passes done", 0, 1), ("passes done -> window staged", 1, 2),
                          ("window staged -> threshold", 2, 7), ("dense: staged -> histogram", 2, 3),
-                         ("dense: histogram -> gathered", 3, 4), ("dense: gathered -> threshold", 4, 5)]:
+                         ("dense: histogram -> bracket", 3, 4), ("dense: bracket -> gathered", 4, 5),
+                         ("dense: gathered -> threshold", 5, 7), ("threshold -> id written", 7, 8)]:
         ok = have(c0) & have(c1) & (st[:, c1] >= st[:, c0])
         if ok.any():
             print(f"{name:34s} ({ok.sum():4d} rows): {pct(rel[ok, c1] - rel[ok, c0])}")
@@ -57,6 +62,9 @@ def row_sampler_table(st, B):
         if sel.any():
             print(f"path {ROW_PATHS.get(code, code)!s:18s}: {sel.sum():4d} rows, entry -> threshold "
                   f"{pct(rel[sel, 7] - rel[sel, 0])}")
+            end = sel & have(8)
+            if end.any():
+                print(f"{'':23s}{end.sum():4d} rows, entry -> id written  {pct(rel[end, 8] - rel[end, 0])}")
 
 
 def main():
@@ -103,9 +111,10 @@ def main():
     if B <= torch.cuda.get_device_properties(dev).multi_processor_count:
         L.lsg_row_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
         L.lsg_row_stamps_read.restype = ctypes.c_int
+        raw = np.zeros(ROWS * ROW_SLOTS, dtype=np.uint64)
         if L.lsg_row_stamps_read(raw.ctypes.data, raw.nbytes) != 0:
             raise SystemExit("lsg_row_stamps_read failed")
-        row_sampler_table(raw.reshape(ROWS, SLOTS)[:B].astype(np.int64), B)
+        row_sampler_table(raw.reshape(ROWS, ROW_SLOTS)[:B].astype(np.int64), B)
         return
     if L.lsg_phase_stamps_read(raw.ctypes.data, raw.nbytes) != 0:
         raise SystemExit("lsg_phase_stamps_read failed")
