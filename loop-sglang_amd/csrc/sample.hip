@@ -1328,8 +1328,8 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
       const float y = X.y(x);
       e[i] = R.has(j) && y > yt ? ex2c(y) : 0.0f;
       const bool in = R.has(j) && y > yb && y <= yt;
-      mj |= in ? (1u << i) : 0u;
       const uint64_t bm = __ballot(in);
+      mj |= (uint32_t)((bm >> lane) & 1ull) << i;  // from the ballot: no flag stays live
       if (bm) {
         const int slot = run + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
