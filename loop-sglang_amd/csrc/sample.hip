@@ -54,7 +54,8 @@ constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
 // of its row to g_row_stamps[b * 8 + slot] (slots: 0 kernel entry, 1 both
 // passes done (barrier 1), 2 candidate window staged, 3 dense path: histogram
 // done, 4 dense path: crossing bracketed, 5 dense path: bracket gathered,
-// 7 threshold known on any path, 8 id written, by the lane writing it); slot 6
+// 7 threshold known on any path, 8 id written, by the lane writing it, 9 dense
+// path: kept masses, 10 inverse-CDF barrier passed); slot 6
 // holds the hardware id (bits 0-31),
 // the XCC id (32-39) and the row's path (40-47: 1 unfiltered walk, 2 window of
 // at most 128, 3 ranked window, 4 dense top-p, 5 exact refinement, 6 argmax).
@@ -921,6 +922,7 @@ __device__ __forceinline__ void cdf_walk(Row<T, NT, CAP, VEC, FULL>& R, double t
   const double ws = wave_sum(tmass);
   if (lane == 0) S.wtot[wid] = ws;
   __syncthreads();
+  row_stamp(10);
   int wstar;
   double base;
   const double U = cross_wave<NW>(lane < NW ? S.wtot[lane] : 0.0, u, &wstar, &base);
@@ -1456,6 +1458,7 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
     }
     tmass += (double)cj;
   }
+  row_stamp(9);
   cdf_walk<true>(R, tmass, cs, [&](int) { return 0.0f; }, [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, u, S,
                  out);
   return true;

@@ -40,7 +40,8 @@ ROW_SLOTS = 16
 def row_sampler_table(st, B):
     """Phases of the one-row-per-workgroup sampler (slots: 0 entry, 1 passes
     done, 2 window staged, 3-5 dense path: histogram, bracket, gather,
-    7 threshold known, 8 id written, 6 ids and path)."""
+    7 threshold known, 8 id written, 9 dense path: kept masses, 10 inverse-CDF
+    barrier passed, 6 ids and path)."""
     info = st[:, 6]
     path_of = (info >> 40) & 0xFF
     base = st[:, 0].min()
@@ -53,7 +54,9 @@ def row_sampler_table(st, B):
     for name, c0, c1 in [("entry -> passes done", 0, 1), ("passes done -> window staged", 1, 2),
                          ("window staged -> threshold", 2, 7), ("dense: staged -> histogram", 2, 3),
                          ("dense: histogram -> bracket", 3, 4), ("dense: bracket -> gathered", 4, 5),
-                         ("dense: gathered -> threshold", 5, 7), ("threshold -> id written", 7, 8)]:
+                         ("dense: gathered -> threshold", 5, 7), ("threshold -> id written", 7, 8),
+                         ("dense: threshold -> kept masses", 7, 9), ("kept masses -> walk barrier", 9, 10),
+                         ("walk barrier -> id written", 10, 8)]:
         ok = have(c0) & have(c1) & (st[:, c1] >= st[:, c0])
         if ok.any():
             print(f"{name:34s} ({ok.sum():4d} rows): {pct(rel[ok, c1] - rel[ok, c0])}")
@@ -65,6 +68,10 @@ def row_sampler_table(st, B):
             end = sel & have(8)
             if end.any():
                 print(f"{'':23s}{end.sum():4d} rows, entry -> id written  {pct(rel[end, 8] - rel[end, 0])}")
+            steps = [("passes", 0, 1), ("window attempt", 1, 2), ("to threshold", 2, 7), ("walk", 7, 8)]
+            print(f"{'':23s}p50 " + ", ".join(
+                f"{nm} {np.median(rel[sel & have(c1), c1] - rel[sel & have(c1), c0]):.2f}"
+                for nm, c0, c1 in steps if (sel & have(c1)).any()))
 
 
 def main():
