@@ -59,3 +59,44 @@ def test_gate_then_greedy(lsg, dev):
         want = torch.argmax(wl["logits"][rows], dim=-1).to(torch.int32)
         assert torch.equal(res.token_ids[:n], want)
         F = res.state
+
+
+def test_lookahead_decode_steps(lsg, orc, dev):
+    """Three core steps with the default lookahead routing: the rows sampled in
+    a step are those whose previous-step request (or the depth cap) routes
+    them, exactly the rows a second gate's exit_route sends out on the same
+    inputs; their tokens match the oracle on those rows; nothing leaves at the
+    first step (no request is pending yet)."""
+    g = torch.Generator(device=dev).manual_seed(41)
+    B, H, V = 384, 512, 8000
+    w = (torch.randn(H, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    b = torch.tensor([-0.5], device=dev).to(torch.bfloat16)
+    gate = lsg.OuroExitGate(w, b, exit_threshold=0.4, loop_steps=4)
+    twin = lsg.OuroExitGate(w, b, exit_threshold=0.4, loop_steps=4)
+    pend, pend_t = gate.init_pending_pool(B), twin.init_pending_pool(B)
+    logits = torch.randn(B, V, generator=g, device=dev) * 2
+    args = lsg.BatchSamplingArgs(torch.full((B,), 0.7, device=dev), None, torch.full((B,), 0.9, device=dev),
+                                 torch.rand(B, generator=g, device=dev))
+    F = F_t = None
+    for step in range(3):
+        h = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
+        res = lsg.cdb_decode_step(gate, h, F, step, logits, args, max_depth=3, pending=pend)
+        ref = twin.exit_route(h, F_t, step, pending=pend_t, max_depth=3)
+        n = int(res.n_exit.item())
+        assert n == int(ref.n_exit.item())
+        assert torch.equal(res.exit_idx[:n], ref.exit_idx[:n])
+        assert torch.equal(res.route, ref.route)
+        if step == 0:
+            assert n == 0
+        if n:
+            rows = res.exit_idx[:n].long()
+            x = logits[rows].cpu().numpy()
+            sel = lambda t: t[rows].cpu().numpy()
+            want, amb, alt = orc.sample(x, sel(args.temperatures), None, sel(args.top_p), sel(args.uniforms),
+                                        with_alt=True)
+            got = res.token_ids[:n].cpu().numpy()
+            excused = ((amb & 1) != 0) | (((amb & 2) != 0) & ((amb & 4) != 0))
+            ok = (got == want) | (((amb & 2) != 0) & (got == alt)) | excused
+            assert ok.all() and excused.sum() <= 2
+        F, F_t = res.state, ref.state
+    assert n > 0  # rows routed by the previous steps' requests or the depth cap
