@@ -383,6 +383,15 @@ def main():
         def launch_gemm(i):
             pkg.coda.lm_head(h, Ws[i % nW], out=lg)
 
+        f32 = torch.empty(B, V, device=dev)
+
+        def launch_flinear(i):  # the reference's projection (hipBLASLt through F.linear)
+            torch.nn.functional.linear(h, Ws[i % nW])
+
+        def launch_ref_flow(i):  # the reference's data flow: bf16 logits -> fp32 buffer -> sampler
+            f32.copy_(torch.nn.functional.linear(h, Ws[i % nW]))
+            pkg.sample_rows(f32, T, Kt, P, U, out=ids)
+
         if a.traffic_probe:
             _probe(torch, launch_gemm, dev)
             return
@@ -391,6 +400,8 @@ def main():
         per = secs / K
         gtimes = _time_graph(torch, launch_gemm, K, W)
         gper = _median(gtimes) / K
+        fper = _median(_time_graph(torch, launch_flinear, K, W)) / K
+        rper = _median(_time_graph(torch, launch_ref_flow, K, W)) / K
         ntiles = -(-V // 192)
         gemm_bytes = V * H * 2 + B * H * 2 + B * V * 2 + B * ntiles * 8  # W, h, bf16 logits, tile maxima
         flops = 2.0 * B * H * V
@@ -427,6 +438,9 @@ def main():
             "projection": {"ms_per_launch": gper * 1e3, "timing": _timing(gtimes, K),
                            "mfma_tflops": flops / gper / 1e12, "mfma_peak_tflops": 2500.0,
                            "mfma_frac": flops / gper / 1e12 / 2500.0},
+            "reference_flow": {"f_linear_ms": fper * 1e3, "f_linear_fp32_copy_sample_ms": rper * 1e3,
+                               "note": "the same graph harness: F.linear (hipBLASLt) alone, and F.linear -> "
+                                       "copy into an fp32 [B, V] buffer -> lsg_sample on fp32"},
             "roofline": {"bound": "hbm", "achieved": gemm_bytes / gper / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gemm_bytes / gper / 1e9 / HBM_PEAK_GBS,
                          "traffic": _traffic_from_profiles(a.workload)},

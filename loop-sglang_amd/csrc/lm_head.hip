@@ -17,12 +17,15 @@
 // lm_head_kernel: C[b, v] = bf16(sum_k h[b, k] * W[v, k]) on MFMA
 // (v_mfma_f32_32x32x16_bf16, fp32 accumulation).  One 256-thread workgroup per
 // (256-row batch tile, 192-column vocabulary tile); W is streamed from HBM once
-// per batch tile, h is re-read from L2.  K advances in steps of 32 through five
-// LDS stages filled by direct-to-LDS loads (no register staging), four stages
-// ahead of the MFMAs, so ~112 KB per compute unit are in flight to cover the
-// memory latency.  A stage row is 64 bytes (four 16-byte chunks), chunk c of
-// row r stored at position c ^ (((r >> 1) ^ (r >> 2)) & 3), so the 16-byte
-// fragment reads of eight (or sixteen) consecutive rows hit distinct banks.  Eight waves (two per SIMD):
+// per batch tile, h is re-read from L2.  K advances in steps of 64 through two
+// LDS stages filled by direct-to-LDS loads (no register staging), one stage
+// ahead of the MFMAs.  The length of each W row's read per stage sets the
+// speed (HBM serves 128-byte row segments far better than 64-byte ones: K
+// steps of 16 / 32 / 64 measured 106 / 76 / 64 us for the Ouro-shaped
+// projection), and two 57 KB stages fill the LDS.  A stage row is 128 bytes
+// (eight 16-byte chunks), chunk c of row r stored at position c ^ ((r >> 1) & 7),
+// so the fragment reads of 16 consecutive rows hit distinct banks.  Eight waves
+// (two per SIMD):
 // wave w owns batch rows 64 (w % 4) .. +63 of the tile and columns
 // 96 (w / 4) .. +95: 2 x 3 blocks of 32 x 32, 96 fp32 accumulators per lane.
 // Operand layouts (checked on the device): A lane l holds row l % 32,
@@ -45,19 +48,23 @@ namespace lmh {
 
 constexpr int kMT = 256;   // batch rows per tile
 constexpr int kNT = 192;   // vocabulary columns per tile
-constexpr int kKT = 32;    // K per stage
-constexpr int kRow = 32;   // LDS row stride in bf16 (64 bytes, swizzled)
-constexpr int kStages = 5;  // LDS stages (four in flight ahead of the MFMAs)
+constexpr int kKT = 64;      // K per stage
+constexpr int kRow = kKT;    // LDS row stride in bf16 (swizzled 16-byte chunks)
+constexpr int kStages = 2;   // LDS stages (all but one in flight ahead of the MFMAs)
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kHalf = kNT / 2;  // columns per wave, and per row-statistics tile
 constexpr int kStageA = kMT * kRow;  // bf16 elements of h per stage
 constexpr int kStageB = kNT * kRow;  // bf16 elements of W per stage
 constexpr int kLdsElems = kStages * (kStageA + kStageB);
-// direct-to-LDS loads per wave per stage, 1 KB (16 rows) each: h's 16 row
-// groups two per wave; W's 12 groups two per wave (waves 4-7 load their own
-// group twice, the same bytes to the same place)
-constexpr int kLoadsA = 2, kLoadsB = 2, kLoads = kLoadsA + kLoadsB;
+// direct-to-LDS loads per wave per stage, 1 KB (kRPG rows of kCPR 16-byte
+// chunks) each: h's and W's row groups spread over the waves (a wave past the
+// last group loads its own group again, the same bytes to the same place)
+constexpr int kCPR = kKT / 8, kRPG = 64 / kCPR;
+constexpr int kGroupsA = kMT / kRPG, kGroupsB = kNT / kRPG;
+constexpr int kLoadsA = (kGroupsA + kWaves - 1) / kWaves, kLoadsB = (kGroupsB + kWaves - 1) / kWaves;
+constexpr int kLoads = kLoadsA + kLoadsB;
+static_assert(kKT % 16 == 0 && kMT % kRPG == 0 && kNT % kRPG == 0, "stage shape");
 // epilogue: 64 rows x 96 columns of bf16 per wave, rows padded by 8
 constexpr int kOutRow = kHalf + 8;
 
@@ -87,31 +94,38 @@ __device__ __forceinline__ float bf2f(uint32_t u16) { return __uint_as_float(u16
 // 16 i: row i / 4, position i % 4), reading the chunk that belongs at that
 // position.  Rows outside the matrices read the last row (their results are
 // never stored).
-__device__ __forceinline__ int swz(int row, int c) { return c ^ (((row >> 1) ^ (row >> 2)) & 3); }
+// A 16-byte LDS read serves 16 lanes at a time: the fragment reads of 16
+// consecutive rows (one chunk each) must fill 16 distinct 16-byte slots of a
+// 256-byte bank line.  A 128-byte row puts rows of one parity in one half of
+// the line, so chunk c of row r goes to position c ^ ((r >> 1) & 7).
+__device__ __forceinline__ int swz(int row, int c) {
+  static_assert(kCPR == 8, "swizzle for 128-byte stage rows");
+  return c ^ ((row >> 1) & 7);
+}
 
 __device__ __forceinline__ void issue_stage(const Params& P, uint16_t* lds, int64_t m0, int64_t n0, int s, int kb) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   uint16_t* A = lds + (s % kStages) * (kStageA + kStageB);
   uint16_t* Bm = A + kStageA;
   const int64_t k0 = (int64_t)kb * kKT;
-  const int rl = lane >> 2, pos = lane & 3;
+  const int rl = lane / kCPR, pos = lane % kCPR;
 #pragma unroll
   for (int q = 0; q < kLoadsA; ++q) {
-    const int g = q * kWaves + wid;
-    const int row = 16 * g + rl;
+    const int g = q * kWaves + wid < kGroupsA ? q * kWaves + wid : wid;
+    const int row = kRPG * g + rl;
     int64_t gr = m0 + row;
     gr = gr < P.B ? gr : P.B - 1;
     const uint16_t* src = P.h + gr * P.ldh + k0 + swz(row, pos) * 8;
-    __builtin_amdgcn_global_load_lds(src, A + 16 * g * kRow, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, A + kRPG * g * kRow, 16, 0, 0);
   }
 #pragma unroll
   for (int q = 0; q < kLoadsB; ++q) {
-    const int g = q == 0 ? wid : (wid < 4 ? wid + kWaves : wid);
-    const int row = 16 * g + rl;
+    const int g = q * kWaves + wid < kGroupsB ? q * kWaves + wid : wid;
+    const int row = kRPG * g + rl;
     int64_t gr = n0 + row;
     gr = gr < P.V ? gr : P.V - 1;
     const uint16_t* src = P.w + gr * P.ldw + k0 + swz(row, pos) * 8;
-    __builtin_amdgcn_global_load_lds(src, Bm + 16 * g * kRow, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src, Bm + kRPG * g * kRow, 16, 0, 0);
   }
 }
 
@@ -119,6 +133,21 @@ __device__ __forceinline__ void issue_stage(const Params& P, uint16_t* lds, int6
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until stage s has landed: at most min(ahead, M) later stages' loads
+// stay outstanding (loads retire in order).
+template <int M>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if constexpr (M > 0) {
+    if (ahead >= M) {
+      wait_vm<M * kLoads>();
+      return;
+    }
+    wait_stages<M - 1>(ahead);
+  } else {
+    wait_vm<0>();
+  }
 }
 
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) void lm_head_kernel(Params P) {
@@ -143,11 +172,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1))) v
     if (q < nst) issue_stage(P, lds, m0, n0, q, kblock(q));
   for (int s = 0; s < nst; ++s) {
     // stage s complete for this wave (loads retire in order), then for all
-    const int ahead = nst - 1 - s;
-    if (ahead >= 3) wait_vm<3 * kLoads>();
-    else if (ahead == 2) wait_vm<2 * kLoads>();
-    else if (ahead == 1) wait_vm<kLoads>();
-    else wait_vm<0>();
+    wait_stages<kStages - 2>(nst - 1 - s);
     __syncthreads();  // also: every wave is done with stage s - 1's buffer
     if (s + kStages - 1 < nst) issue_stage(P, lds, m0, n0, s + kStages - 1, kblock(s + kStages - 1));
     const uint16_t* A = lds + (s % kStages) * (kStageA + kStageB);
