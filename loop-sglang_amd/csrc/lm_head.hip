@@ -65,6 +65,10 @@ constexpr int kGroupsA = kMT / kRPG, kGroupsB = kNT / kRPG;
 constexpr int kLoadsA = (kGroupsA + kWaves - 1) / kWaves, kLoadsB = (kGroupsB + kWaves - 1) / kWaves;
 constexpr int kLoads = kLoadsA + kLoadsB;
 static_assert(kKT % 16 == 0 && kMT % kRPG == 0 && kNT % kRPG == 0, "stage shape");
+// every wave's first load has a row group of its own (a wave past the last
+// group reloads its own group, which must exist): fewer groups than waves
+// would put rows past the stage
+static_assert(kGroupsA >= kWaves && kGroupsB >= kWaves, "at least one row group per wave");
 // epilogue: 64 rows x 96 columns of bf16 per wave, rows padded by 8
 constexpr int kOutRow = kHalf + 8;
 
