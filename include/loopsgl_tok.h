@@ -110,7 +110,7 @@ int lsg_exit_gate(const void* h, int dtype, int64_t B, int64_t H, int64_t ldh, c
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has
  * no counterpart in the reference.  Same arguments and results as lsg_exit_gate
  * without the workspace: the compaction uses a static device array inside the
- * library (one per GPU, about 128 KiB, held until the process ends), looked up
+ * library (one per GPU, about 64 KiB, held until the process ends), looked up
  * for the current device, which must be the stream's device.
  *   B             at most 65536 rows (LSG_ERR_ARG beyond).
  * Calls that overlap in time on one GPU share that array and race: serialise

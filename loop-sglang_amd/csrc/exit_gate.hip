@@ -29,7 +29,7 @@
 
 namespace lsg {
 
-constexpr int kGateThreads = 256;
+constexpr int kGateThreads = 512;
 constexpr int kGateRows = kGateThreads / kWave;  // one wave per row
 // Published word of a workgroup: serial << 32 | state << 30 | count.
 constexpr unsigned long long kStateAgg = 1ull << 30;  // count of its own rows
