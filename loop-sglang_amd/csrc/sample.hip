@@ -1213,13 +1213,16 @@ __device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t l
 // candidate window (near-flat rows keep thousands of elements).  One compute
 // unit holds the row, so every full pass costs a few microseconds; the path
 // makes two:
-//   1. a count histogram of the members (elements with y > -32) over bins of
-//      1/128 binary order of y (one LDS add per element, no exponential).
-//      Every element of bin b weighs within a factor 2^(1/256) of
-//      2^(-(b + 1/2)/128), and over a bin the errors largely cancel, so the
-//      exact crossing of p * Z lies, but for rows with masses piled at bin
-//      edges, between the first bins where the estimate reaches
-//      p * Z (1 -+ 2^-12) (a block scan, every thread holding four bins);
+//   1. a histogram of the members (elements with y > -32) over bins of 1/64
+//      binary order of y: per bin the count and the sum of the members'
+//      offsets inside the bin (16-bit fixed point), one 64-bit LDS add per
+//      element, no exponential.  A bin's mass is estimated as
+//      count * 2^(-(b + mean offset)/64): the first-order error cancels, the
+//      rest is below (ln 2 / 128)^2 / 2 ~ 1.5e-5 of the bin's mass whatever the
+//      values (bf16 rows at low temperature put their members on a few
+//      distinct offsets per bin), so the exact crossing of p * Z lies between
+//      the first bins where the estimate reaches p * Z (1 -+ 2^-12) (a block
+//      scan, every thread holding two bins);
 //   2. one pass over the register chunks: each chunk's mass above the bracket
 //      (the float sums the inverse CDF uses) to the chunk-mass array, and the
 //      members inside the bracket to per-wave LDS segments (a wave-uniform
@@ -1234,8 +1237,9 @@ __device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t l
 // changed) when the bracket misses the crossing or a segment overflows.
 // Every wave calls it together.
 // ---------------------------------------------------------------------------
-constexpr int kDenseRes = 128, kDenseOrders = 32;
-constexpr int kDenseBins = kDenseRes * kDenseOrders;  // 4096
+constexpr int kDenseRes = 64, kDenseOrders = 32;
+constexpr int kDenseBins = kDenseRes * kDenseOrders;  // 2048
+constexpr int kDenseCountShift = 44;                  // bin word: count << 44 | sum of 16-bit offsets
 
 template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, double Z, float p, float u,
@@ -1247,15 +1251,15 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
   static_assert(BPT * NT == kDenseBins && BPT >= 1, "bins split evenly over the threads");
   static_assert(CAP * EPV <= 64, "member positions fit one 64-bit mask");
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(csum);
+  unsigned long long* hist = reinterpret_cast<unsigned long long*>(csum);
   const float ylo = -(float)kDenseOrders;
-  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0u;
+  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0ull;
   if (t == 0) {
     S.rbin = -1;                 // bracket top bin (none yet)
     S.pick = kDenseBins - 1;     // bracket bottom bin
   }
   __syncthreads();
-  // members: ylo < y <= 0, so bin = trunc(-128 y) lies in [0, kDenseBins)
+  // members: ylo < y <= 0, so bin = trunc(-64 y) lies in [0, kDenseBins)
 #pragma unroll
   for (int j = 0; j < CAP; ++j) {
     if (R.has(j) && X.y(R.cm_at(j)) > ylo) {
@@ -1264,7 +1268,12 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
 #pragma unroll
       for (int i = 0; i < EPV; ++i) {
         const float y = X.y(Elem<T>::get(v, i));
-        if (y > ylo) atomicAdd(&hist[(int)(-(float)kDenseRes * y)], 1u);
+        if (y > ylo) {
+          const float tb = -(float)kDenseRes * y;  // exact: a power-of-two scale
+          const int b = (int)tb;
+          const uint32_t off = (uint32_t)((tb - (float)b) * 65536.0f);  // offset in the bin, < 2^16
+          atomicAdd(&hist[b], (1ull << kDenseCountShift) + off);
+        }
       }
     }
   }
@@ -1274,14 +1283,14 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
   const double target = (double)p * Z;
   const double tL = target * (1.0 - 1.0 / 4096.0), tU = target * (1.0 + 1.0 / 4096.0);
   float est[BPT];
-  {
-    const float r1 = 0.99459839f;  // 2^(-1/128)
-    float f = ex2c(-((float)(BPT * t) + 0.5f) / (float)kDenseRes);
 #pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      est[q] = (float)hist[BPT * t + q] * f;
-      f *= r1;
-    }
+  for (int q = 0; q < BPT; ++q) {
+    const unsigned long long hv = hist[BPT * t + q];
+    const uint32_t cnt = (uint32_t)(hv >> kDenseCountShift);
+    const float osum = (float)(hv & ((1ull << kDenseCountShift) - 1ull));
+    // mean offset of the members, the truncation of each offset added back
+    const float mo = cnt ? osum / (65536.0f * (float)cnt) + 0.5f / 65536.0f : 0.0f;
+    est[q] = (float)cnt * ex2c(-((float)(BPT * t + q) + mo) / (float)kDenseRes);
   }
   float ts = 0.0f;
 #pragma unroll
@@ -1834,7 +1843,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   // is within the parity tolerance whichever way it falls.
   // (rows of up to six register chunks per thread: with more, the chunks and
   // the path's state exceed the 64 registers of a two-workgroup CU)
-  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(uint32_t)) {
+  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(unsigned long long)) {
     if (!kon && dense_topp(R, X, Z, A.p, A.u, S, csum, out)) return;
   }
   const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
