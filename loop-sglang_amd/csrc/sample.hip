@@ -1830,9 +1830,28 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     if (window_threshold<NT>(S, nw, kon, A.k, pon, A.p, Z, X, &thr)) {
       row_stamp(7);
       row_stamp_path(kRowRanked);
-      tmass = masked_masses(R, X, thr, cs);
-      cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; },
-                      [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, A.u, S, out);
+      if constexpr (FULL != kStream && CAP <= 6) {
+        // rows whose register chunks stay live for the dense top-p path: the
+        // kept masses and the walk read the registers, not memory
+        tmass = 0.0;
+#pragma unroll
+        for (int j = 0; j < CAP; ++j) {
+          float sj = 0.0f;
+          if (R.has(j) && R.cm_at(j) >= thr) {
+            uint4 v = R.d[j];
+            launder(v);
+            sj = esum_chunk_ge<T>(v, X, thr);
+          }
+          cs[j * NT] = sj;
+          tmass += (double)sj;
+        }
+        cdf_walk<true>(R, tmass, cs, [&](int) { return 0.0f; },
+                       [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, A.u, S, out);
+      } else {
+        tmass = masked_masses(R, X, thr, cs);
+        cdf_walk<false>(R, tmass, cs, [&](int) { return 0.0f; },
+                        [&](float x) { return x >= thr ? X.e(x) : 0.0f; }, A.u, S, out);
+      }
       return;
     }
   }
