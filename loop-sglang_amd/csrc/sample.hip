@@ -1214,15 +1214,19 @@ __device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t l
 // unit holds the row, so every full pass costs a few microseconds; the path
 // makes two:
 //   1. a histogram of the members (elements with y > -32) over bins of 1/64
-//      binary order of y: per bin the count and the sum of the members'
-//      offsets inside the bin (16-bit fixed point), one 64-bit LDS add per
-//      element, no exponential.  A bin's mass is estimated as
-//      count * 2^(-(b + mean offset)/64): the first-order error cancels, the
-//      rest is below (ln 2 / 128)^2 / 2 ~ 1.5e-5 of the bin's mass whatever the
-//      values (bf16 rows at low temperature put their members on a few
-//      distinct offsets per bin), so the exact crossing of p * Z lies between
-//      the first bins where the estimate reaches p * Z (1 -+ 2^-12) (a block
-//      scan, every thread holding two bins);
+//      binary order of y: per bin the count (bits 20-31) and the sum of the
+//      members' offsets inside the bin (8-bit fixed point, bits 0-19), one
+//      32-bit LDS add per element, no exponential.  A bin's mass is estimated
+//      as count * 2^(-(b + mean offset)/64): the first-order error cancels, the
+//      rest (second order, ~1.5e-5, and the offsets' quantisation, ~2e-5) is
+//      far below 2^-12 of the bin's mass whatever the values (bf16 rows at low
+//      temperature put their members on a few distinct offsets per bin), so
+//      the exact crossing of p * Z lies between the first bins where the
+//      estimate reaches p * Z (1 -+ 2^-12) (a block scan, every thread holding
+//      two bins).  A bin of more than 4095 members wraps its word: its
+//      estimate is then wrong, the check in step 3 fails and the exact
+//      refinement decides (such rows are nearly constant, and overflow the
+//      member segments anyway);
 //   2. one pass over the register chunks: each chunk's mass above the bracket
 //      (the float sums the inverse CDF uses) to the chunk-mass array, and the
 //      members inside the bracket to per-wave LDS segments (a wave-uniform
@@ -1239,7 +1243,7 @@ __device__ __forceinline__ uint32_t chunk_max_floor(R_& R, int32_t k, uint32_t l
 // ---------------------------------------------------------------------------
 constexpr int kDenseRes = 64, kDenseOrders = 32;
 constexpr int kDenseBins = kDenseRes * kDenseOrders;  // 2048
-constexpr int kDenseCountShift = 44;                  // bin word: count << 44 | sum of 16-bit offsets
+constexpr int kDenseCountShift = 20;                  // bin word: count << 20 | sum of 8-bit offsets
 
 template <typename T, int NT, int CAP, bool VEC, int FULL>
 __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const Ex& X, double Z, float p, float u,
@@ -1251,9 +1255,9 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
   static_assert(BPT * NT == kDenseBins && BPT >= 1, "bins split evenly over the threads");
   static_assert(CAP * EPV <= 64, "member positions fit one 64-bit mask");
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  unsigned long long* hist = reinterpret_cast<unsigned long long*>(csum);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(csum);
   const float ylo = -(float)kDenseOrders;
-  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0ull;
+  for (int i = t; i < kDenseBins; i += NT) hist[i] = 0u;
   if (t == 0) {
     S.rbin = -1;                 // bracket top bin (none yet)
     S.pick = kDenseBins - 1;     // bracket bottom bin
@@ -1271,8 +1275,8 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
         if (y > ylo) {
           const float tb = -(float)kDenseRes * y;  // exact: a power-of-two scale
           const int b = (int)tb;
-          const uint32_t off = (uint32_t)((tb - (float)b) * 65536.0f);  // offset in the bin, < 2^16
-          atomicAdd(&hist[b], (1ull << kDenseCountShift) + off);
+          const uint32_t off = (uint32_t)((tb - (float)b) * 256.0f);  // offset in the bin, < 2^8
+          atomicAdd(&hist[b], (1u << kDenseCountShift) + off);
         }
       }
     }
@@ -1285,11 +1289,11 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
   float est[BPT];
 #pragma unroll
   for (int q = 0; q < BPT; ++q) {
-    const unsigned long long hv = hist[BPT * t + q];
-    const uint32_t cnt = (uint32_t)(hv >> kDenseCountShift);
-    const float osum = (float)(hv & ((1ull << kDenseCountShift) - 1ull));
+    const uint32_t hv = hist[BPT * t + q];
+    const uint32_t cnt = hv >> kDenseCountShift;
+    const float osum = (float)(hv & ((1u << kDenseCountShift) - 1u));
     // mean offset of the members, the truncation of each offset added back
-    const float mo = cnt ? osum / (65536.0f * (float)cnt) + 0.5f / 65536.0f : 0.0f;
+    const float mo = cnt ? osum / (256.0f * (float)cnt) + 0.5f / 256.0f : 0.0f;
     est[q] = (float)cnt * ex2c(-((float)(BPT * t + q) + mo) / (float)kDenseRes);
   }
   float ts = 0.0f;
@@ -1862,7 +1866,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
   // is within the parity tolerance whichever way it falls.
   // (rows of up to six register chunks per thread: with more, the chunks and
   // the path's state exceed the 64 registers of a two-workgroup CU)
-  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(unsigned long long)) {
+  if constexpr (FULL != kStream && CAP <= 6 && NT * CAP * sizeof(float) >= kDenseBins * sizeof(uint32_t)) {
     if (!kon && dense_topp(R, X, Z, A.p, A.u, S, csum, out)) return;
   }
   const uint32_t klo = bin >= 0 ? (uni(S.kmin) >> SH)
