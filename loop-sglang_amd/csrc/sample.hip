@@ -51,7 +51,7 @@ constexpr double kBinMargin = 1.0 + 1.0 / 1024.0;
 
 // Phase stamps, compiled in only by the profiling build (-DLSG_PHASE_STAMPS):
 // thread 0 of workgroup b writes the 100 MHz real-time counter at fixed points
-// of its row to g_row_stamps[b * 8 + slot] (slots: 0 kernel entry, 1 both
+// of its row to g_row_stamps[b * kRowStampSlots + slot] (slots: 0 kernel entry, 1 both
 // passes done (barrier 1), 2 candidate window staged, 3 dense path: histogram
 // done, 4 dense path: crossing bracketed, 5 dense path: bracket gathered,
 // 7 threshold known on any path, 8 id written, by the lane writing it, 9 dense

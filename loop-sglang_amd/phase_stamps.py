@@ -4,6 +4,8 @@ Build the profiling library first (here, not on the GPU):
     python loop-sglang_amd/build.py --stamps
 then, on the GPU:
     python loop-sglang_amd/phase_stamps.py [--workload sample_huginn] [--nbuf 5]
+(`--workload coda_ouro` samples the bf16 logits of the package's LM head on the
+fused-coda inputs.)
 
 The profiling build (libloopsgl_tok_stamps.so, -DLSG_PHASE_STAMPS) has thread 0
 of every workgroup of the streamed-row sampler (or, for batches of no more rows
@@ -46,7 +48,9 @@ def row_sampler_table(st, B):
     path_of = (info >> 40) & 0xFF
     base = st[:, 0].min()
     rel = (st - base) * 0.01
-    have = lambda c: st[:, c] > 0
+    # slots a row's path does not write keep values of earlier launches: count a stamp only when it
+    # is not earlier than the row's own entry stamp
+    have = lambda c: (st[:, c] > 0) & (st[:, c] >= st[:, 0])
     pct = lambda v: "p50 %6.2f  p90 %6.2f  max %6.2f" % (np.median(v), np.percentile(v, 90), v.max())
     print("kernel entry (rel. first):", pct(rel[:, 0]))
     print("threshold known (rel. first):", pct(rel[have(7), 7]))
@@ -74,9 +78,35 @@ def row_sampler_table(st, B):
                 for nm, c0, c1 in steps if (sel & have(c1)).any()))
 
 
+def coda_logits(torch, pkg, dev, nbuf):
+    """bf16 logits [256, 49152] of the package's LM head (lsg_lm_head) on the fused-coda bench inputs:
+    h ~ N(0, 1) [256, 2048], W ~ N(0, 0.02^2) [49152, 2048] (one W per buffer, drawn in the bench's
+    order from the same seeded generator), with the bench's temperatures, top-k, top-p and uniforms."""
+    B, H, V = 256, 2048, 49152
+    g = torch.Generator(device=dev).manual_seed(1)
+    h = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
+    bufs = []
+    for _ in range(3):  # the bench draws three weight copies before the sampling arguments
+        W = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        bufs.append(pkg.coda.lm_head(h, W))
+        del W
+    T = 0.3 + 0.9 * torch.rand(B, generator=g, device=dev)
+    Kt = torch.tensor([1, 20, 50, V], dtype=torch.int32, device=dev)[
+        torch.randint(0, 4, (B,), generator=g, device=dev)].contiguous()
+    P = 0.8 + 0.2 * torch.rand(B, generator=g, device=dev)
+    U = torch.rand(B, generator=g, device=dev)
+    g2 = torch.Generator(device=dev).manual_seed(2)
+    while len(bufs) < nbuf:  # further buffers: more weight draws of the same distribution
+        W = (torch.randn(V, H, generator=g2, device=dev) * 0.02).to(torch.bfloat16)
+        bufs.append(pkg.coda.lm_head(h, W))
+        del W
+    return bufs[:nbuf], (T, Kt, P, U)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", default="sample_huginn", choices=["sample_huginn", "sample_ouro", "cdb_mixed_depth"])
+    ap.add_argument("--workload", default="sample_huginn",
+                    choices=["sample_huginn", "sample_ouro", "cdb_mixed_depth", "coda_ouro"])
     ap.add_argument("--nbuf", type=int, default=5)
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--lib", default=os.path.join(HERE, "libloopsgl_tok_stamps.so"),
@@ -96,11 +126,14 @@ def main():
     L.lsg_phase_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
     L.lsg_phase_stamps_read.restype = ctypes.c_int
     dev = torch.device("cuda:0")
-    make = getattr(pkg.workloads, a.workload)
-    wl = make(dev, seed=3 if a.workload == "sample_huginn" else 1)
-    bufs = [wl["logits"]] + [make(dev, seed=100 + i)["logits"] for i in range(a.nbuf - 1)]
-    args = (wl["temperatures"], wl.get("top_k"), wl["top_p"], wl["uniforms"])
-    B = wl["logits"].shape[0]
+    if a.workload == "coda_ouro":
+        bufs, args = coda_logits(torch, pkg, dev, a.nbuf)
+    else:
+        make = getattr(pkg.workloads, a.workload)
+        wl = make(dev, seed=3 if a.workload == "sample_huginn" else 1)
+        bufs = [wl["logits"]] + [make(dev, seed=100 + i)["logits"] for i in range(a.nbuf - 1)]
+        args = (wl["temperatures"], wl.get("top_k"), wl["top_p"], wl["uniforms"])
+    B = bufs[0].shape[0]
     for i in range(2 * a.nbuf):
         pkg.sample_rows(bufs[i % a.nbuf], *args)
     torch.cuda.synchronize()
