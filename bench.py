@@ -16,7 +16,7 @@ Prints one JSON line (metric / value / roofline / cpu_baseline ...).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                   [--no-cpu-baseline]
-Workloads: sample_huginn (default), sample_ouro, gate_cdb, cdb_mixed_depth.
+Workloads: sample_huginn (default), sample_ouro, gate_cdb, cdb_mixed_depth, coda_ouro.
 
 HBM traffic per launch (the roofline's "traffic" field) comes from two
 rocprofv3 counter runs of the probe mode, then the summary mode:

@@ -42,6 +42,11 @@ constexpr int kBins = 64;  // histogram of y = log2(e / e_max): bins of width 1/
 constexpr int kRefBins = 256;             // exact refinement: bins per level
 constexpr double kFix = 1099511627776.0;  // exact refinement: mass fixed point, 2^40
 constexpr float kYMin = -32.0f;  // y covered by the histogram: [kYMin, 0]
+// Scale of the per-wave mass histogram's 32-bit words.  A bin b collects at most
+// 128 chunk maxima of mass <= 2^(-b/2) (<= 1 relative to the wave maximum) and
+// 64 chunk remainders (EPV - 1) 2^ye with ye <= -1 in bins >= 2 (<= 3.5 each):
+// at most 288, below 2^32 / 2^23 = 512.
+constexpr float kWaveMassFix = 0x1p23f;
 // Margin on the top-p histogram test: the bin is chosen where the float sum of
 // the binned maxima reaches p*Z*(1 + 2^-10), so the window (a superset of those
 // maxima, summed in double) always reaches p*Z despite the rounding of the
@@ -323,7 +328,7 @@ struct Smem {
   float wmax[NW];   // per-wave maxima
   int hcnt[kBins];
   float hmass[kBins];
-  uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass as float bits)
+  uint32_t wh[NW][kBins];  // per-wave histograms (count, or mass in kWaveMassFix fixed point)
   uint32_t kmin;           // smallest order key in the candidate window
   unsigned long long rbins[4][kRefBins + 1];  // exact refinement: bin copies by lane, one bin apart in bank order
   int rk_cnt[2 * kWave];    // small window: entries at or above each entry
@@ -1518,7 +1523,10 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     // Histogram, relative to this wave's maximum, of the two largest chunk
     // maxima of each thread (distinct elements): count (top-k) or mass
     // (top-p) per bin of y = log2(mass).  Merged into the row's histogram
-    // after the barrier.
+    // after the barrier.  Masses are added as truncated fixed-point integers
+    // (32-bit integer LDS adds: on near-flat rows every lane's maxima share a
+    // few bins, and float LDS adds to them took ~1.7 us longer); truncation
+    // only lowers a bin's mass, so the floor stays a lower bound.
     typename Row<T, NT, CAP, VEC, FULL>::CM cmv;
     cmv.load(R.cmx);
     float y1 = -INFINITY, y2 = -INFINITY;
@@ -1531,11 +1539,11 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
     uint32_t* h = S.wh[wid];
     if (y1 >= kYMin) {
       if (kon) atomicAdd(&h[ybin(y1)], 1u);
-      else atomicAdd(reinterpret_cast<float*>(&h[ybin(y1)]), ex2c(y1));
+      else atomicAdd(&h[ybin(y1)], (uint32_t)(ex2c(y1) * kWaveMassFix));
     }
     if (y2 >= kYMin) {
       if (kon) atomicAdd(&h[ybin(y2)], 1u);
-      else atomicAdd(reinterpret_cast<float*>(&h[ybin(y2)]), ex2c(y2));
+      else atomicAdd(&h[ybin(y2)], (uint32_t)(ex2c(y2) * kWaveMassFix));
     }
     if (!kon && y1 >= kYMin) {
       // The chunk of largest mass M (n = EPV elements, thread maximum m): at
@@ -1546,7 +1554,7 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       // still get a bound.
       const float rest = cmx - ex2c(y1);
       const float ye = rest > 0.0f ? __log2f(rest * (0.5f / (float)(EPV - 1))) : -INFINITY;
-      if (ye >= kYMin) atomicAdd(reinterpret_cast<float*>(&h[ybin(ye)]), 0.5f * rest);
+      if (ye >= kYMin) atomicAdd(&h[ybin(ye)], (uint32_t)(0.5f * rest * kWaveMassFix));
     }
   }
   __syncthreads();
@@ -1623,7 +1631,8 @@ __device__ __forceinline__ void row_sample_fused(Row<T, NT, CAP, VEC, FULL>& R, 
       for (int q = 0; q < NW; ++q) pc += lane >= sqs[q] ? (int)v[q] : 0;
     } else {
 #pragma unroll
-      for (int q = 0; q < NW; ++q) pmf = __builtin_fmaf(__uint_as_float(v[q]), lane >= sqs[q] ? fqs[q] : 0.0f, pmf);
+      for (int q = 0; q < NW; ++q)
+        pmf = __builtin_fmaf((float)v[q] * (1.0f / kWaveMassFix), lane >= sqs[q] ? fqs[q] : 0.0f, pmf);
     }
     const int pcs = wave_incl_scan_i(pc, lane);
     const double pm = wave_incl_scan((double)pmf, lane);
