@@ -1278,10 +1278,10 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
       for (int i = 0; i < EPV; ++i) {
         const float y = X.y(Elem<T>::get(v, i));
         if (y > ylo) {
-          const float tb = -(float)kDenseRes * y;  // exact: a power-of-two scale
-          const int b = (int)tb;
-          const uint32_t off = (uint32_t)((tb - (float)b) * 256.0f);  // offset in the bin, < 2^8
-          atomicAdd(&hist[b], (1u << kDenseCountShift) + off);
+          // q = floor(-64 * 256 y) (a power-of-two scale, exact): bin q >> 8,
+          // the 8-bit offset inside the bin q & 255
+          const uint32_t q = (uint32_t)(-(float)(kDenseRes * 256) * y);
+          atomicAdd(&hist[q >> 8], (1u << kDenseCountShift) | (q & 255u));
         }
       }
     }
