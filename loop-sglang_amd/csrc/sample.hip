@@ -141,6 +141,12 @@ struct Ex {
   __device__ __forceinline__ float y(float x) const {
     return fma ? __builtin_fmaf(x, c, nb) : (x - gm) * c;
   }
+  // y(x) for a known form (FMA == fma): one instruction per element instead
+  // of both forms and a select
+  template <bool FMA>
+  __device__ __forceinline__ float yf(float x) const {
+    return FMA ? __builtin_fmaf(x, c, nb) : (x - gm) * c;
+  }
   __device__ __forceinline__ float e(float x) const { return ex2c(y(x)); }
 };
 
@@ -1269,23 +1275,28 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
   }
   __syncthreads();
   // members: ylo < y <= 0, so bin = trunc(-64 y) lies in [0, kDenseBins)
+  auto hist_pass = [&](auto form) {
+    constexpr bool FMA = decltype(form)::value;
 #pragma unroll
-  for (int j = 0; j < CAP; ++j) {
-    if (R.has(j) && X.y(R.cm_at(j)) > ylo) {
-      uint4 v = R.d[j];
-      launder(v);
+    for (int j = 0; j < CAP; ++j) {
+      if (R.has(j) && X.y(R.cm_at(j)) > ylo) {
+        uint4 v = R.d[j];
+        launder(v);
 #pragma unroll
-      for (int i = 0; i < EPV; ++i) {
-        const float y = X.y(Elem<T>::get(v, i));
-        if (y > ylo) {
-          // q = floor(-64 * 256 y) (a power-of-two scale, exact): bin q >> 8,
-          // the 8-bit offset inside the bin q & 255
-          const uint32_t q = (uint32_t)(-(float)(kDenseRes * 256) * y);
-          atomicAdd(&hist[q >> 8], (1u << kDenseCountShift) | (q & 255u));
+        for (int i = 0; i < EPV; ++i) {
+          const float y = X.template yf<FMA>(Elem<T>::get(v, i));
+          if (y > ylo) {
+            // q = floor(-64 * 256 y) (a power-of-two scale, exact): bin q >> 8,
+            // the 8-bit offset inside the bin q & 255
+            const uint32_t q = (uint32_t)(-(float)(kDenseRes * 256) * y);
+            atomicAdd(&hist[q >> 8], (1u << kDenseCountShift) | (q & 255u));
+          }
         }
       }
     }
-  }
+  };
+  if (X.fma) hist_pass(std::true_type{});
+  else hist_pass(std::false_type{});
   __syncthreads();
   row_stamp(3);
   // block scan of the estimates (thread t: bins BPT*t ..)
@@ -1336,32 +1347,36 @@ __device__ __forceinline__ bool dense_topp(Row<T, NT, CAP, VEC, FULL>& R, const 
   float* cs = csum + t;
   double above = 0.0;
   uint64_t inm = 0ull;  // bit j * EPV + i: element i of chunk j lies in the bracket
+  // (the generic y here: a copy per form spills registers)
+  auto gather_pass = [&]() {
 #pragma unroll
-  for (int j = 0; j < CAP; ++j) {
-    uint4 v = R.d[j];
-    launder(v);
-    float e[EPV];
-    uint32_t mj = 0u;
+    for (int j = 0; j < CAP; ++j) {
+      uint4 v = R.d[j];
+      launder(v);
+      float e[EPV];
+      uint32_t mj = 0u;
 #pragma unroll
-    for (int i = 0; i < EPV; ++i) {
-      const float x = Elem<T>::get(v, i);
-      const float y = X.y(x);
-      e[i] = R.has(j) && y > yt ? ex2c(y) : 0.0f;
-      const bool in = R.has(j) && y > yb && y <= yt;
-      const uint64_t bm = __ballot(in);
-      mj |= (uint32_t)((bm >> lane) & 1ull) << i;  // from the ballot: no flag stays live
-      if (bm) {
-        const int slot = run + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
-                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
-        if (in && slot < kSegC) seg[slot] = okey(x);
-        run += (int)__popcll(bm);
+      for (int i = 0; i < EPV; ++i) {
+        const float x = Elem<T>::get(v, i);
+        const float y = X.y(x);
+        e[i] = R.has(j) && y > yt ? ex2c(y) : 0.0f;
+        const bool in = R.has(j) && y > yb && y <= yt;
+        const uint64_t bm = __ballot(in);
+        mj |= (uint32_t)((bm >> lane) & 1ull) << i;  // from the ballot: no flag stays live
+        if (bm) {
+          const int slot = run + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+          if (in && slot < kSegC) seg[slot] = okey(x);
+          run += (int)__popcll(bm);
+        }
       }
+      inm |= (uint64_t)mj << (j * EPV);
+      const float cj = tree_sum<EPV>(e);
+      cs[j * NT] = cj;
+      above += (double)cj;
     }
-    inm |= (uint64_t)mj << (j * EPV);
-    const float cj = tree_sum<EPV>(e);
-    cs[j * NT] = cj;
-    above += (double)cj;
-  }
+  };
+  gather_pass();
   above = wave_sum(above);
   if (lane == 0) {
     S.wtot[wid] = above;
