@@ -119,9 +119,12 @@ __device__ __forceinline__ unsigned long long fix40(float e) {
 // Exponent map of one row: e(x) = 2^y(x), y(x) = (x - m) * c with c = log2(e)/T.
 // When |m*c| < 2^22, y is one fma against b = m*c rounded up: every exponent is
 // then <= 0 and all of them carry the same offset m*c - b in [-1/2, 0], which
-// cancels in every ratio.  Otherwise y = (x - m) * c.
+// cancels in every ratio.  Otherwise y = (x - m) * c.  Both forms are
+// fma(x - sa, c, sb): sa = 0, sb = -b for the first (x - 0 is x), sa = m,
+// sb = 0 for the second (the product rounded once; only a -0 product turns
+// into +0, which every use of y treats alike).
 struct Ex {
-  float c, nb, gm;
+  float c, nb, gm, sa, sb;
   bool fma;
   __device__ __forceinline__ void init(float gm_, float c_) {
     gm = gm_;
@@ -129,6 +132,8 @@ struct Ex {
     const float b = mul_up(gm, c);
     fma = __builtin_fabsf(b) < 4194304.0f;
     nb = -b;
+    sa = fma ? 0.0f : gm;
+    sb = fma ? nb : 0.0f;
   }
   // Same for wave-uniform arguments; the fields are kept in scalar registers.
   __device__ __forceinline__ void init_u(float gm_, float c_) {
@@ -137,10 +142,11 @@ struct Ex {
     const float b = uni(mul_up(gm, c));
     fma = __builtin_fabsf(b) < 4194304.0f;
     nb = -b;
+    sa = uni(fma ? 0.0f : gm);
+    sb = uni(fma ? nb : 0.0f);
   }
-  __device__ __forceinline__ float y(float x) const {
-    return fma ? __builtin_fmaf(x, c, nb) : (x - gm) * c;
-  }
+  // two instructions per element whatever the form (no select between forms)
+  __device__ __forceinline__ float y(float x) const { return __builtin_fmaf(x - sa, c, sb); }
   // y(x) for a known form (FMA == fma): one instruction per element instead
   // of both forms and a select
   template <bool FMA>
