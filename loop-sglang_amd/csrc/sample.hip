@@ -1962,6 +1962,8 @@ void sampler_kernel(SampleParams P) {
 //   chunks per row NV <= 256*8    256 threads, 8 chunks each in registers
 //   NV == 1024*6 (e.g. 49152 bf16) 1024 threads, exactly 6 full chunks each
 //   NV <= 1024*8                  1024 threads, 8 chunks each (two per CU)
+//   NV == 1024*12 (49152 fp32)    1024 threads, exactly 12 full chunks each
+//                                 (16 chunks spill registers)
 //   NV <= 1024*16                 1024 threads, 16 chunks each (one per CU)
 //   longer rows                   1024 threads, 16 chunks each, the rest streamed
 // Unaligned rows (row start or stride not 16-byte aligned) use element loads.
@@ -1980,6 +1982,7 @@ static void launch_rows(const SampleParams& P, bool vec, hipStream_t st) {
   else if (NV == 1024 * 8 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 8, true, kFull, 8>, 1024, P, st);
   else if (NV == 1024 * 6 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 6, true, kFull, 8>, 1024, P, st);
   else if (NV <= 1024 * 8) launch(sampler_kernel<G, T, 1024, 8, true, kBounded, 8>, 1024, P, st);
+  else if (NV == 1024 * 12 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 12, true, kFull, 4>, 1024, P, st);
   else if (NV == 1024 * 16 && P.V % EPV == 0) launch(sampler_kernel<G, T, 1024, 16, true, kFull, 4>, 1024, P, st);
   else if (NV <= 1024 * 16) launch(sampler_kernel<G, T, 1024, 16, true, kBounded, 4>, 1024, P, st);
   else launch(sampler_kernel<G, T, 1024, 16, true, kStream, 4>, 1024, P, st);

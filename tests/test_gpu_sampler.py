@@ -162,10 +162,12 @@ def test_flat_rows_exact_path(lsg, orc, dev):
     check_sampling(lsg, orc, x, T, K, P, U, max_excused=1)
 
 
-@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 49152), (torch.float16, 49152), (torch.float32, 24576)])
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 49152), (torch.float16, 49152), (torch.float32, 24576),
+                                     (torch.float32, 49152)])
 def test_dense_topp_rows(lsg, orc, dev, dtype, V):
     """Top-p rows whose kept set holds thousands of elements (B=64 <= CUs:
-    one row per CU, six register chunks per thread): the mass histogram, the
+    one row per CU, six register chunks per thread; twelve for fp32 V=49152,
+    whose rows take the exact refinement instead): the mass histogram, the
     crossing bin's members and their key radix.  Rows: near-flat Gaussian at
     several T and p (0.05 .. 0.999), thresholds near x = 0 (wide key span in
     the crossing bin), NaN and -inf elements, half the row tied at one value,
